@@ -1,0 +1,221 @@
+/*
+ * pcdevice.h -- C ABI of libpcdevice_hip, the MI355X (gfx950) implementation
+ * of the batched predictive-coding relaxation of matteofabbri/PredicitiveCoding
+ * (PredictiveCoding.Device/BatchedPcForward.cs) and of the device runtime
+ * calls that path makes.
+ *
+ * Conventions, following the reference's P/Invoke layer
+ * (PredictiveCoding.Device/Interop/Cuda.cs:16-50, Cublas.cs:25-59):
+ *   - every entry point is cdecl and returns an int status (0 = success); the
+ *     codes are the reference's DeviceStatus enum (Interop/CudaStatus.cs:7-19);
+ *   - handles come back through out-pointers;
+ *   - host buffers are read during the call only and never retained
+ *     (DeviceTensor.cs:94-120);
+ *   - device pointers are HIP device memory (pcd_malloc_async, or any other
+ *     HIP allocation in the same process);
+ *   - work is queued on the given stream (NULL = the device's null stream)
+ *     and is complete only after a synchronisation.
+ * Thread safety: distinct streams may be used from distinct threads; a model
+ * handle is immutable after creation; the per-call scratch belongs to the
+ * (model, stream) pair.
+ */
+#ifndef PCDEVICE_H
+#define PCDEVICE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* DeviceStatus, Interop/CudaStatus.cs:7-19 (CudaError/CublasError carry HIP
+ * runtime and GEMM failures here). */
+enum pcd_status {
+    PCD_SUCCESS = 0,
+    PCD_NOT_INITIALIZED = 1,
+    PCD_NO_DEVICE = 2,
+    PCD_OUT_OF_MEMORY = 3,
+    PCD_INVALID_VALUE = 4,
+    PCD_HIP_ERROR = 5,
+    PCD_GEMM_ERROR = 6,
+    PCD_COLLECTIVE_ERROR = 7, /* unused: no multi-GPU path */
+    PCD_NOT_SUPPORTED = 8,
+    PCD_UNKNOWN = 100
+};
+
+/* MemcpyKind, Interop/Cuda.cs:6 */
+enum pcd_memcpy_kind {
+    PCD_HOST_TO_HOST = 0,
+    PCD_HOST_TO_DEVICE = 1,
+    PCD_DEVICE_TO_HOST = 2,
+    PCD_DEVICE_TO_DEVICE = 3,
+    PCD_MEMCPY_DEFAULT = 4
+};
+
+/* ActivationType, PredicitiveCoding/Core/Activation.cs:19-25, extended with
+ * the tanh-approximation GELU used throughout the reference
+ * (PredictiveCoding.LLM/Model/Layers.cs:42-50). */
+enum pcd_activation {
+    PCD_ACT_LINEAR = 0,
+    PCD_ACT_TANH = 1,
+    PCD_ACT_RELU = 2,
+    PCD_ACT_SIGMOID = 3,
+    PCD_ACT_GELU = 4
+};
+
+/* Storage/operand type of the weights and of the GEMM operands.
+ *   PCD_F32   fp32 everything (InferGetTopBatch, mixed = false)
+ *   PCD_F16   weights and both GEMM operands rounded to fp16, fp32 accumulate,
+ *             fp32 states/errors/energy (the reference's mixed = true,
+ *             Gemm.cs:44-60, CudaGemmProvider.cs:150-202)
+ *   PCD_BF16  as PCD_F16 with bf16 round-to-nearest-even
+ *             (TensorUtils.cs:379-401) */
+enum pcd_dtype { PCD_F32 = 0, PCD_BF16 = 1, PCD_F16 = 2 };
+
+/* Early-exit rule of the ragged entry point.
+ *   PCD_EXIT_NONE      run every request for its full step budget
+ *   PCD_EXIT_RELATIVE  Network.SettleAdaptive (Network.cs:876-907): stop after
+ *                      a step once prev - E < thr * max(prev, 1e-12); the
+ *                      first step never exits
+ *   PCD_EXIT_ABSOLUTE  stop after a step once E / rows_of_request < thr
+ * E is the request's energy summed over its rows, read before the update of
+ * the step (Network.cs:939-945 over Layer.cs:437-450). */
+enum pcd_exit_rule { PCD_EXIT_NONE = 0, PCD_EXIT_RELATIVE = 1, PCD_EXIT_ABSOLUTE = 2 };
+
+typedef struct pcd_model pcd_model;
+
+/* ---------------------------------------------------------------- runtime */
+
+/* cudaGetDeviceCount, Interop/Cuda.cs:23; DeviceRuntime probing
+ * (DeviceRuntime.cs:27-32,68-82): no GPU gives *count = 0 and PCD_NO_DEVICE. */
+int pcd_get_device_count(int* count);
+/* cudaSetDevice, Interop/Cuda.cs:24 */
+int pcd_set_device(int device);
+int pcd_get_device(int* device);
+/* cudaDeviceSynchronize, Interop/Cuda.cs:25 */
+int pcd_device_synchronize(void);
+/* Text of the calling thread's last failure (empty if none). Replaces the
+ * exception message NativeCheck.Ok builds (CudaStatus.cs:22-38). */
+int pcd_last_error(char* buf, size_t len);
+/* Library version as major*10000 + minor*100 + patch. */
+int pcd_version(int* version);
+
+/* ----------------------------------------------------------------- memory */
+
+/* Pooled device allocation: IDeviceAllocator.Allocate/Free
+ * (Allocators/IDeviceAllocator.cs:6-18) as CudaAllocator implements them
+ * (Allocators/CudaAllocator.cs:32-59): power-of-two buckets of at most 32
+ * cached blocks, stream-ordered allocation with a synchronous fallback. */
+int pcd_malloc_async(void** ptr, size_t bytes, void* stream);
+int pcd_free_async(void* ptr, void* stream);
+/* Pinned host memory: CudaAllocator.AllocatePinnedHost/FreePinnedHost
+ * (CudaAllocator.cs:63-84). */
+int pcd_host_alloc(void** ptr, size_t bytes);
+int pcd_host_free(void* ptr);
+/* Releases every cached block of both pools (CudaAllocator.TrimPools). */
+int pcd_trim_pools(void);
+/* cudaMemcpy / cudaMemcpyAsync / cudaMemsetAsync, Interop/Cuda.cs:37-39 */
+int pcd_memcpy(void* dst, const void* src, size_t bytes, int kind);
+int pcd_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream);
+int pcd_memset_async(void* dst, int value, size_t bytes, void* stream);
+
+/* -------------------------------------------------------- streams, events */
+
+/* CudaStreamManager.CreateStream/Synchronize (Streams/CudaStreamManager.cs:38-52)
+ * over cudaStreamCreate/Destroy/Synchronize (Interop/Cuda.cs:42-44).  Streams
+ * are created non-blocking at the default priority. */
+int pcd_stream_create(void** stream);
+int pcd_stream_destroy(void* stream);
+int pcd_stream_synchronize(void* stream);
+/* RecordEvent/WaitEvent (CudaStreamManager.cs:62-75) over the event calls of
+ * Interop/Cuda.cs:45-48, plus the elapsed time between two events. */
+int pcd_event_create(void** event);
+int pcd_event_record(void* event, void* stream);
+int pcd_event_synchronize(void* event);
+int pcd_event_destroy(void* event);
+int pcd_event_elapsed_ms(float* ms, void* start, void* end);
+
+/* ------------------------------------------------------------------- GEMM */
+
+/* Row-major C[m,n] = op(A) op(B) + beta C on device pointers, the semantics of
+ * CudaGemmProvider.MatMulDeviceEx (Gemm/CudaGemmProvider.cs:82-98): op(A) is
+ * A [m,k] or, with trans_a, the transpose of a physical [k,m] A (same for B).
+ * With trans_a = trans_b = 0 and beta = 0 this is MatMulDevice (:62-72).
+ * Scratch for operand packing comes from the library's pool. */
+int pcd_gemm_f32(const float* dA, const float* dB, float* dC, int m, int k, int n,
+                 int trans_a, int trans_b, float beta, void* stream);
+/* bf16 operands (raw bf16 bit patterns), fp32 accumulation and fp32 C:
+ * CudaGemmProvider.MatMulDeviceExBf16 (CudaGemmProvider.cs:107-127). */
+int pcd_gemm_bf16(const uint16_t* dA, const uint16_t* dB, float* dC, int m, int k, int n,
+                  int trans_a, int trans_b, float beta, void* stream);
+/* fp16 operands: CudaGemmProvider.MatMulMixedDevice (CudaGemmProvider.cs:185-202). */
+int pcd_gemm_f16(const uint16_t* dA, const uint16_t* dB, float* dC, int m, int k, int n,
+                 int trans_a, int trans_b, float beta, void* stream);
+
+/* --------------------------------------------------------- PC relaxation */
+
+/* Uploads a GenerativeSnapshot (Networks/GenerativeSnapshot.cs:15-23) to the
+ * current device.
+ *   sizes[levels]       LayerSizes, levels >= 2
+ *   W[levels-1]         host pointers; W[l-1] is W_l [sizes[l-1] x sizes[l]] row-major
+ *   b[levels-1]         host pointers; b[l-1] is b_l [sizes[l-1]]
+ *   precisions[levels]  scalar precision per layer (> 0)
+ *   eta, act_reg        StateLearningRate, ActivityRegularization (>= 0)
+ *   ffg                 UseFeedforwardGistInit
+ *   dtype               enum pcd_dtype
+ * The library keeps its own device copies (W and W^T in the operand dtype,
+ * biases in fp32); host memory is read during the call only. */
+int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta, float act_reg, int ffg,
+                        const float* const* W, const float* const* b, const float* precisions,
+                        int dtype, pcd_model** out);
+int pcd_pc_model_destroy(pcd_model* model);
+
+/* BatchedPcForward.InferGetTopBatch (BatchedPcForward.cs:36-139): settles
+ * `batch` samples for `steps` steps from zero free states, layer 0 clamped to
+ * x0.  All pointers are device pointers.
+ *   x0          [batch x sizes[0]]
+ *   out_top     [batch x sizes[levels-1]]
+ *   out_states  nullable; every layer l = 0..levels-1 as [batch x sizes[l]],
+ *               concatenated in layer order
+ *   out_energy  nullable; [steps x batch] per-sample energy of each step
+ * Errors: PCD_INVALID_VALUE for batch < 1 ("Empty batch.", :44), steps < 1
+ * (:45) or null pointers.  (The per-input length check of :55-57 is the
+ * caller's, since x0 arrives packed.)  Asynchronous on `stream`. */
+int pcd_pc_relax(pcd_model* model, const float* x0, int batch, int steps,
+                 float* out_top, float* out_states, float* out_energy, void* stream);
+
+/* Ragged request batches: request r owns rows [row_offsets[r], row_offsets[r+1])
+ * of x0_packed and settles for at most steps[r] steps, leaving early by
+ * exit_rule / exit_threshold (enum pcd_exit_rule) -- Network.InferAdaptive
+ * (Network.cs:760-782) applied per request, all requests in one packed launch.
+ * Device pointers:
+ *   x0_packed   [rows x sizes[0]], rows = row_offsets[requests]
+ *   out_top     [rows x sizes[levels-1]]
+ * Host pointers (read or written during the call, which synchronises `stream`):
+ *   row_offsets [requests+1] increasing, row_offsets[0] = 0
+ *   steps       [requests]   each >= 1
+ *   steps_used  [requests]   steps each request ran
+ *   out_energy  [requests]   nullable; the request's energy at its last step
+ */
+int pcd_pc_relax_ragged(pcd_model* model, const float* x0_packed, const int* row_offsets, const int* steps,
+                        int requests, int exit_rule, float exit_threshold, int* steps_used,
+                        float* out_top, float* out_energy, void* stream);
+
+/* Model properties (levels, sizes, dtype) for host wrappers. */
+int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_sizes, int* dtype);
+
+/* Relaxation options (no counterpart in the reference; tuning and profiling
+ * hooks for the host wrappers and the benchmark):
+ *   use_graph    capture the T-step loop in a hipGraph (default 1)
+ *   tile_m/n     force a GEMM tile (0 = automatic choice)
+ *   profile      record per-kernel HIP events on the next eager run */
+int pcd_pc_set_option(pcd_model* model, const char* name, int value);
+/* Average duration (ms) of the error-phase and update-phase kernels over the
+ * launches of the last profiled call, and their launch counts. */
+int pcd_pc_profile_result(pcd_model* model, float* error_phase_ms, float* update_phase_ms, int* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PCDEVICE_H */

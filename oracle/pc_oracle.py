@@ -1,0 +1,194 @@
+"""ctypes binding of ``libpcoracle.so`` (the C restatement in ``pc_oracle.c``).
+
+Test infrastructure only: imported by tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of bench.py.  Every function mirrors a reference
+routine cited in ``pc_oracle.c``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libpcoracle.so")
+_lib = None
+
+ACT = {"linear": 0, "tanh": 1, "relu": 2, "sigmoid": 3, "gelu": 4}
+ROUND = {"none": 0, "f16": 1, "bf16": 2}
+EXIT = {"none": 0, "relative": 1, "absolute": 2}
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_vp = ctypes.c_void_p
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile; returns the library path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.pco_act_apply_f32.argtypes = [ctypes.c_int, _f32p, _f32p, ctypes.c_long]
+        L.pco_act_deriv_f32.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, ctypes.c_long]
+        L.pco_act_apply_f64.argtypes = [ctypes.c_int, _f64p, _f64p, ctypes.c_long]
+        L.pco_act_deriv_f64.argtypes = [ctypes.c_int, _f64p, _f64p, _f64p, ctypes.c_long]
+        L.pco_round.argtypes = [ctypes.c_int, _f32p, _f32p, ctypes.c_long]
+        L.pco_bf16_bits.argtypes = [_f32p, _u16p, ctypes.c_long]
+        L.pco_gemm.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_int, _f32p, ctypes.c_int]
+        L.pco_set_threads.argtypes = [ctypes.c_int]
+        L.pco_get_threads.restype = ctypes.c_int
+        L.pco_batched_relax.argtypes = [
+            _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+            _f32p, _f32p, _f32p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int, _f32p, _vp, _vp]
+        L.pco_batched_relax.restype = ctypes.c_int
+        L.pco_ragged_relax.argtypes = [
+            _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+            _f32p, _f32p, _f32p, ctypes.c_int, _f32p, _i32p, _i32p, ctypes.c_int,
+            ctypes.c_int, ctypes.c_float, _i32p, _f32p, _f32p]
+        L.pco_ragged_relax.restype = ctypes.c_int
+        L.pco_persample_relax_f64.argtypes = [
+            _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_int,
+            _f64p, _f64p, _f64p, _f64p, ctypes.c_int, ctypes.c_int, _f64p, _vp, _vp]
+        L.pco_persample_relax_f64.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def set_threads(n: int) -> None:
+    lib().pco_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().pco_get_threads())
+
+
+def act_apply(act: str, x, dtype=np.float32):
+    x = np.ascontiguousarray(x, dtype=dtype)
+    y = np.empty_like(x)
+    fn = lib().pco_act_apply_f32 if dtype == np.float32 else lib().pco_act_apply_f64
+    fn(ACT[act], x.ravel(), y.ravel(), x.size)
+    return y
+
+
+def act_deriv(act: str, pre, dtype=np.float32):
+    pre = np.ascontiguousarray(pre, dtype=dtype)
+    y = act_apply(act, pre, dtype)
+    d = np.empty_like(pre)
+    fn = lib().pco_act_deriv_f32 if dtype == np.float32 else lib().pco_act_deriv_f64
+    fn(ACT[act], pre.ravel(), y.ravel(), d.ravel(), pre.size)
+    return d
+
+
+def round16(mode: str, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().pco_round(ROUND[mode], x.ravel(), y.ravel(), x.size)
+    return y
+
+
+def bf16_bits(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    b = np.empty(x.shape, dtype=np.uint16)
+    lib().pco_bf16_bits(x.ravel(), b.ravel(), x.size)
+    return b
+
+
+def gemm(a, b, round_mode: str = "none"):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    c = np.empty((m, n), dtype=np.float32)
+    lib().pco_gemm(a.ravel(), m, k, b.ravel(), n, c.ravel(), ROUND[round_mode])
+    return c
+
+
+def _flat(arrs, dtype):
+    if not arrs:
+        return np.zeros(1, dtype=dtype)
+    return np.ascontiguousarray(np.concatenate([np.asarray(a, dtype=dtype).ravel() for a in arrs]))
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def batched_relax(sizes, act, eta, weights, biases, precisions, x0, steps,
+                  act_reg=0.0, ffg=False, round_mode="none", want_states=False, want_energy=False):
+    """BatchedPcForward.InferGetTopBatch in fp32 (optionally with 16-bit operand
+    rounding).  Returns (top [B,s_top], states list or None, energy [T,B] or None)."""
+    sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+    x0 = np.ascontiguousarray(x0, dtype=np.float32)
+    B = x0.shape[0]
+    top = np.empty((B, int(sizes[-1])), dtype=np.float32)
+    states = np.empty(B * int(sizes.sum()), dtype=np.float32) if want_states else None
+    energy = np.empty((steps, B), dtype=np.float32) if want_energy else None
+    rc = lib().pco_batched_relax(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg),
+                                 _flat(weights, np.float32), _flat(biases, np.float32),
+                                 np.ascontiguousarray(precisions, dtype=np.float32), ROUND[round_mode],
+                                 x0.ravel(), B, int(steps), top.ravel(), _ptr(states), _ptr(energy))
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    st = None
+    if want_states:
+        st, off = [], 0
+        for s in sizes:
+            st.append(states[off:off + B * int(s)].reshape(B, int(s)))
+            off += B * int(s)
+    return top, st, energy
+
+
+def persample_relax_f64(sizes, act, eta, weights, biases, precisions, x0, steps,
+                        act_reg=0.0, ffg=False, want_states=False, want_energy=False):
+    """Network.InferGetTop(x, steps, resetState: true) per sample, in float64."""
+    sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+    x0 = np.ascontiguousarray(x0, dtype=np.float64)
+    B = x0.shape[0]
+    top = np.empty((B, int(sizes[-1])), dtype=np.float64)
+    states = np.empty(B * int(sizes.sum()), dtype=np.float64) if want_states else None
+    energy = np.empty((steps, B), dtype=np.float64) if want_energy else None
+    rc = lib().pco_persample_relax_f64(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg),
+                                       _flat(weights, np.float64), _flat(biases, np.float64),
+                                       np.ascontiguousarray(precisions, dtype=np.float64),
+                                       x0.ravel(), B, int(steps), top.ravel(), _ptr(states), _ptr(energy))
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    st = None
+    if want_states:
+        st, off = [], 0
+        for s in sizes:
+            st.append(states[off:off + B * int(s)].reshape(B, int(s)))
+            off += B * int(s)
+    return top, st, energy
+
+
+def ragged_relax(sizes, act, eta, weights, biases, precisions, x0_packed, row_offsets, steps,
+                 exit_rule="none", exit_thr=0.0, act_reg=0.0, ffg=False, round_mode="none"):
+    """Per-request settling with early exit; returns (steps_used, final_energy, top)."""
+    sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+    x0 = np.ascontiguousarray(x0_packed, dtype=np.float32)
+    offs = np.ascontiguousarray(row_offsets, dtype=np.int32)
+    st = np.ascontiguousarray(steps, dtype=np.int32)
+    R = len(st)
+    used = np.zeros(R, dtype=np.int32)
+    fe = np.zeros(R, dtype=np.float32)
+    top = np.zeros((x0.shape[0], int(sizes[-1])), dtype=np.float32)
+    rc = lib().pco_ragged_relax(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg),
+                                _flat(weights, np.float32), _flat(biases, np.float32),
+                                np.ascontiguousarray(precisions, dtype=np.float32), ROUND[round_mode],
+                                x0.ravel(), offs, st, R, EXIT[exit_rule], exit_thr, used, fe, top.ravel())
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    return used, fe, top

@@ -1,0 +1,178 @@
+"""BatchedPcForward on MI355X: the reference entry point over libpcdevice_hip.
+
+``BatchedPcForward.infer_get_top_batch`` keeps the signature, argument checks
+and semantics of BatchedPcForward.InferGetTopBatch
+(PredictiveCoding.Device/BatchedPcForward.cs:36-139): settle every input from
+zero free states with layer 0 clamped, return the top latent per sample.
+``mixed=True`` selects 16-bit GEMM operands with fp32 accumulation; like the
+reference (Gemm.cs:44-60) that is fp16 unless ``dtype="bf16"`` is asked for.
+
+``PcDeviceModel`` is the device-resident model (pcd_pc_model_create) with the
+extended entry points: all final states, per-step energies, device-pointer
+I/O for benchmarks, and ragged request batches with early exit.
+"""
+from __future__ import annotations
+
+import ctypes
+import weakref
+
+import numpy as np
+
+from . import _native
+from ._native import DTYPE, EXIT, MEMCPY, call
+from .device import DeviceTensor, Stream
+from .errors import ArgumentException, ArgumentNullException, ArgumentOutOfRangeException
+from .snapshot import GenerativeSnapshot
+
+
+class PcDeviceModel:
+    """A GenerativeSnapshot uploaded to the current GPU in one operand dtype."""
+
+    def __init__(self, snapshot: GenerativeSnapshot, dtype: str = "f32"):
+        if dtype not in DTYPE:
+            raise ArgumentException(f"dtype must be one of {sorted(DTYPE)}")
+        self.snapshot = snapshot
+        self.dtype = dtype
+        L = len(snapshot.layer_sizes)
+        self.sizes = list(snapshot.layer_sizes)
+        sizes = (ctypes.c_int * L)(*self.sizes)
+        wp = (ctypes.c_void_p * (L - 1))(*[w.ctypes.data for w in snapshot.weights])
+        bp = (ctypes.c_void_p * (L - 1))(*[b.ctypes.data for b in snapshot.biases])
+        prec = (ctypes.c_float * L)(*snapshot.precisions)
+        h = ctypes.c_void_p()
+        call("pcd_pc_model_create", sizes, L, int(snapshot.activation), float(snapshot.state_learning_rate),
+             float(snapshot.activity_regularization), int(bool(snapshot.use_feedforward_gist_init)),
+             wp, bp, prec, DTYPE[dtype], ctypes.byref(h))
+        self.handle = h.value
+        self._finalizer = weakref.finalize(self, _native.lib().pcd_pc_model_destroy, self.handle)
+
+    def close(self) -> None:
+        self._finalizer()
+        self.handle = None
+
+    def set_option(self, name: str, value: int) -> None:
+        call("pcd_pc_set_option", self.handle, name.encode(), int(value))
+
+    def profile_result(self):
+        e, u, n = ctypes.c_float(), ctypes.c_float(), ctypes.c_int()
+        call("pcd_pc_profile_result", self.handle, ctypes.byref(e), ctypes.byref(u), ctypes.byref(n))
+        return e.value, u.value, n.value
+
+    # ---------------------------------------------------------- device I/O
+
+    def relax_device(self, x0_ptr: int, batch: int, steps: int, out_top_ptr: int,
+                     out_states_ptr: int | None = None, out_energy_ptr: int | None = None,
+                     stream: Stream | None = None) -> None:
+        """pcd_pc_relax on device pointers, queued on `stream` (no sync)."""
+        call("pcd_pc_relax", self.handle, x0_ptr, int(batch), int(steps), out_top_ptr,
+             out_states_ptr, out_energy_ptr, stream.handle if stream else None)
+
+    # ------------------------------------------------------------ host I/O
+
+    def relax(self, x0: np.ndarray, steps: int, want_states: bool = False, want_energy: bool = False,
+              stream: Stream | None = None):
+        """Settle a [batch x s_0] host batch; returns (top, states, energy)."""
+        x0 = np.ascontiguousarray(x0, dtype=np.float32)
+        if x0.ndim != 2 or x0.shape[1] != self.sizes[0]:
+            raise ArgumentException(f"inputs must be [batch x {self.sizes[0]}]")
+        B = x0.shape[0]
+        if B < 1:
+            raise ArgumentException("Empty batch.")
+        if steps < 1:
+            raise ArgumentOutOfRangeException("inferenceSteps")
+        dx = DeviceTensor.from_host(x0)
+        top = DeviceTensor((B, self.sizes[-1]))
+        st = DeviceTensor((B * sum(self.sizes),)) if want_states else None
+        en = DeviceTensor((steps, B)) if want_energy else None
+        try:
+            self.relax_device(dx.ptr, B, steps, top.ptr, st.ptr if st else None, en.ptr if en else None, stream)
+            if stream:
+                stream.synchronize()
+            else:
+                call("pcd_device_synchronize")
+            top_h = top.to_host()
+            states = None
+            if st is not None:
+                flat, states, off = st.to_host(), [], 0
+                for s in self.sizes:
+                    states.append(flat[off:off + B * s].reshape(B, s))
+                    off += B * s
+            energy = en.to_host() if en is not None else None
+        finally:
+            for t in (dx, top, st, en):
+                if t is not None:
+                    t.free()
+        return top_h, states, energy
+
+    def relax_ragged(self, x0_packed: np.ndarray, row_offsets, steps, exit_rule: str = "none",
+                     exit_threshold: float = 0.0, stream: Stream | None = None):
+        """Ragged requests with early exit; returns (steps_used, final_energy, top)."""
+        x0 = np.ascontiguousarray(x0_packed, dtype=np.float32)
+        offs = np.ascontiguousarray(row_offsets, dtype=np.int32)
+        st = np.ascontiguousarray(steps, dtype=np.int32)
+        R = len(st)
+        if R < 1:
+            raise ArgumentException("Empty batch.")
+        if len(offs) != R + 1 or offs[0] != 0 or np.any(np.diff(offs) < 1) or offs[-1] != x0.shape[0]:
+            raise ArgumentException("row_offsets must start at 0, increase strictly and end at the row count")
+        if np.any(st < 1):
+            raise ArgumentOutOfRangeException("steps")
+        if exit_rule not in EXIT:
+            raise ArgumentException(f"exit_rule must be one of {sorted(EXIT)}")
+        rows = int(offs[-1])
+        dx = DeviceTensor.from_host(x0)
+        top = DeviceTensor((rows, self.sizes[-1]))
+        used = np.zeros(R, dtype=np.int32)
+        fe = np.zeros(R, dtype=np.float32)
+        try:
+            call("pcd_pc_relax_ragged", self.handle, dx.ptr,
+                 offs.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), st.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                 R, EXIT[exit_rule], float(exit_threshold), used.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                 top.ptr, fe.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), stream.handle if stream else None)
+            top_h = top.to_host()
+        finally:
+            dx.free()
+            top.free()
+        return used, fe, top_h
+
+
+class BatchedPcForward:
+    """Drop-in for the reference's static class (BatchedPcForward.cs:28-139)."""
+
+    _cache: dict = {}
+
+    @staticmethod
+    def _model(snapshot: GenerativeSnapshot, dtype: str) -> PcDeviceModel:
+        key = (id(snapshot), dtype)
+        hit = BatchedPcForward._cache.get(key)
+        if hit is not None and hit[0]() is snapshot:
+            return hit[1]
+        m = PcDeviceModel(snapshot, dtype)
+        BatchedPcForward._cache[key] = (weakref.ref(snapshot), m)
+        return m
+
+    @staticmethod
+    def infer_get_top_batch(model: GenerativeSnapshot, inputs, inference_steps: int, mixed: bool = False,
+                            dtype: str | None = None):
+        """Settle every input for `inference_steps` steps; returns the top
+        latent of each sample (a list of 1-D float32 arrays)."""
+        if model is None:
+            raise ArgumentNullException("model")
+        if inputs is None:
+            raise ArgumentNullException("inputs")
+        if len(inputs) == 0:
+            raise ArgumentException("Empty batch.")
+        if inference_steps < 1:
+            raise ArgumentOutOfRangeException("inferenceSteps")
+        s0 = model.layer_sizes[0]
+        rows = []
+        for i, x in enumerate(inputs):
+            x = np.asarray(x, dtype=np.float32).ravel()
+            if x.size != s0:
+                raise ArgumentException(f"Input {i} has {x.size} elements; the model expects {s0}.")
+            rows.append(x)
+        if dtype is None:
+            dtype = "f16" if mixed else "f32"
+        dev = BatchedPcForward._model(model, dtype)
+        top, _, _ = dev.relax(np.stack(rows), inference_steps)
+        return [top[i].copy() for i in range(top.shape[0])]

@@ -1,0 +1,534 @@
+// pc_kernels.hpp -- gfx950 kernels of the batched predictive-coding relaxation.
+//
+// One relaxation step of BatchedPcForward.cs:93-128 is two grouped launches:
+//
+//   error phase   for every layer l = 1..L-1 at once (independent problems):
+//                   PRE  = S_l . W_l^T           MFMA GEMM [B x s_{l-1}], K = s_l
+//                   pred = f(PRE + b_l)
+//                   e    = P_{l-1} (M_{l-1} - pred)         -> E_{l-1} (fp32)
+//                   d    = f'(PRE + b_l) * e                -> D_l (operand type)
+//                   energy partial 0.5 e^2 / P_{l-1}, summed per row
+//   update phase  for every layer l = 1..L-1 at once:
+//                   G    = D_l . W_l                 MFMA GEMM [B x s_l], K = s_{l-1}
+//                   M_l -= eta (E_l - G + lambda sign(M_l))  (E_{L-1} = 0)
+//                   S_l  = operand-type copy of M_l
+//
+// Both GEMMs read their operands K-contiguous ("A . B^T" with A [rows x K] and
+// B [N x K] row-major): the error phase uses W_l as stored ([s_{l-1} x s_l]),
+// the update phase a transposed copy W_l^T ([s_l x s_{l-1}]) made once at
+// model upload (the reference transposes every call, BatchedPcForward.cs:62-64).
+// The two phases are the Jacobi order of Network.cs:91-110: every error is
+// computed from the pre-step states before any state moves.
+//
+// Tiling: a 256-thread workgroup (4 waves, 2 x 2) owns a BM x BN output tile;
+// each wave owns (BM/2) x (BN/2) as 32 x 32 MFMA blocks.  K advances in
+// stages of 128 bytes per row staged through LDS (double buffered, one
+// barrier per stage), 16-byte units XOR-swizzled by row so that the 16-byte
+// fragment reads of a wave hit distinct banks.
+//   16-bit operands: v_mfma_f32_32x32x16_{bf16,f16}; lane l holds 8 consecutive
+//     K values of row (l % 32), half-wave l/32 takes the second 8 of each 16.
+//   fp32 operands:   v_mfma_f32_32x32x2f32 x 4 per 32-byte chunk: lane l holds 4
+//     consecutive floats of row (l % 32); MFMA s uses float s of every lane,
+//     so one MFMA sums K indices {c*8+s, c*8+4+s}.
+// Result layout (32x32 blocks): register r of lane l is
+//   row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+// Lambdas inside kernels must inline, or arrays they touch (the MFMA
+// accumulators) lose their registers to the closure's memory.
+#define PCD_INLINE __attribute__((always_inline))
+
+namespace pcd {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Keeps
+// accumulator indices constant however large the body, where #pragma unroll
+// is only a request the unroller may decline.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+enum Act { ACT_LINEAR = 0, ACT_TANH = 1, ACT_RELU = 2, ACT_SIGMOID = 3, ACT_GELU = 4 };
+enum Epi { EPI_ERROR = 0, EPI_UPDATE = 1, EPI_FFG = 2, EPI_PLAIN = 3 };
+
+// bf16 and fp16 are carried as raw 16-bit patterns.
+struct bf16_t { uint16_t v; };
+struct f16_t { uint16_t v; };
+
+// One GEMM of a grouped launch plus the operands of its epilogue.
+struct Problem {
+    const void* A;        // [>= tiles_m*BM rows x lda], K-contiguous
+    const void* B;        // [>= tiles_n*BN rows x ldb], K-contiguous
+    int lda, ldb;         // leading dimensions, elements
+    int M, N, K;          // valid rows, valid columns, K (a multiple of the stage depth)
+    int tiles_m, tiles_n, tile_start;
+    int ldo;              // leading dimension of every [rows x N] epilogue operand
+    const float* bias;    // ERROR/FFG: b_l [N]
+    const float* mlow;    // ERROR: fp32 state M_{l-1}
+    float* eout;          // ERROR: E_{l-1} (nullable: layer 0 is never updated)
+    void* dout;           // ERROR: D_l in the operand type; FFG: operand-type state copy
+    float* m;             // UPDATE: fp32 state M_l (in/out); FFG: state out; PLAIN: C
+    void* mop;            // UPDATE: operand-type copy of M_l (nullable for fp32)
+    const float* eself;   // UPDATE: E_l (nullable for the top layer)
+    float prec;           // ERROR: P_{l-1}
+    int slot_base;        // ERROR: first energy partial slot of this problem
+};
+
+// Problems of one grouped launch, passed by value in the kernel arguments.
+constexpr int kMaxProblems = 16;
+struct ProblemSet {
+    Problem p[kMaxProblems];
+    int n;
+};
+
+static_assert(sizeof(Problem) % 8 == 0, "Problem is copied as 64-bit words");
+struct ProblemWords { uint64_t w[sizeof(Problem) / 8]; };
+
+// Copy one problem out of the kernarg segment (address space 4) word by word.
+__device__ __forceinline__ Problem load_problem(const __attribute__((address_space(4))) Problem* src) {
+    typedef const __attribute__((address_space(4))) uint64_t KWord;
+    KWord* w = (KWord*)src;
+    ProblemWords pw;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(Problem) / 8); ++i) pw.w[i] = w[i];
+    return __builtin_bit_cast(Problem, pw);
+}
+
+struct PhaseArgs {
+    int act;
+    float eta, act_reg;
+    float alpha, beta;          // PLAIN
+    float* energy_part;         // [nslots x ldp] per-row partial energies (nullable)
+    int ldp, nslots;
+    float* energy_out;          // UPDATE prologue: row energies of step t (nullable)
+    int batch, t;
+    const int* row_req;         // ragged: request of each row (nullable)
+    const int* done_at;         // ragged: first step a request no longer runs
+};
+
+// ------------------------------------------------------------ scalar helpers
+
+__device__ __forceinline__ float act_f(int act, float x) {
+    switch (act) {
+    case ACT_TANH: return tanhf(x);
+    case ACT_RELU: return x > 0.f ? x : 0.f;
+    case ACT_SIGMOID: return 1.f / (1.f + expf(-x));
+    case ACT_GELU: return 0.5f * x * (1.f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
+    default: return x;
+    }
+}
+
+// f'(pre) given y = f(pre): Activation.cs:86-132; GELU from pre (Autograd.cs:313-318).
+__device__ __forceinline__ float act_df(int act, float pre, float y) {
+    switch (act) {
+    case ACT_TANH: return 1.f - y * y;
+    case ACT_RELU: return pre > 0.f ? 1.f : 0.f;
+    case ACT_SIGMOID: return y * (1.f - y);
+    case ACT_GELU: {
+        const float c = 0.7978845608f, a = 0.044715f;
+        float t = tanhf(c * (pre + a * pre * pre * pre));
+        return 0.5f * (1.f + t) + 0.5f * pre * (1.f - t * t) * (c * (1.f + 3.f * a * pre * pre));
+    }
+    default: return 1.f;
+    }
+}
+
+// Round-to-nearest-even fp32 -> bf16 with NaN kept NaN (TensorUtils.cs:386-395).
+__device__ __forceinline__ uint16_t to_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ uint16_t to_f16(float x) {
+    _Float16 h = (_Float16)x;  // v_cvt_f16_f32, round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+template <typename OP> struct OpTraits;
+template <> struct OpTraits<float> {
+    static constexpr int bytes = 4;
+    __device__ static void store(void* base, size_t idx, float v) { ((float*)base)[idx] = v; }
+};
+template <> struct OpTraits<bf16_t> {
+    static constexpr int bytes = 2;
+    __device__ static void store(void* base, size_t idx, float v) { ((uint16_t*)base)[idx] = to_bf16(v); }
+};
+template <> struct OpTraits<f16_t> {
+    static constexpr int bytes = 2;
+    __device__ static void store(void* base, size_t idx, float v) { ((uint16_t*)base)[idx] = to_f16(v); }
+};
+
+// One 32-byte K chunk of a 32x32 block: a and b hold this lane's 16 bytes.
+template <typename OP> __device__ __forceinline__ void mfma_chunk(f32x16& acc, const u32x4& a, const u32x4& b);
+template <> __device__ __forceinline__ void mfma_chunk<float>(f32x16& acc, const u32x4& a, const u32x4& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[0]), __uint_as_float(b[0]), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[1]), __uint_as_float(b[1]), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[2]), __uint_as_float(b[2]), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[3]), __uint_as_float(b[3]), acc, 0, 0, 0);
+}
+template <> __device__ __forceinline__ void mfma_chunk<bf16_t>(f32x16& acc, const u32x4& a, const u32x4& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+}
+template <> __device__ __forceinline__ void mfma_chunk<f16_t>(f32x16& acc, const u32x4& a, const u32x4& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
+}
+
+// Workgroup ids are dealt round-robin over the 8 XCDs; renumber them so that
+// consecutive logical tiles (which share operand rows) run on one XCD and
+// share its L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+    const int X = 8;
+    int q = nblocks / X, r = nblocks % X;
+    int x = bid % X, i = bid / X;
+    return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+}
+
+// Row activity of the ragged path: the row's request still runs at step t.
+__device__ __forceinline__ bool row_active(const PhaseArgs& a, int row) {
+    return a.row_req == nullptr || a.t < a.done_at[a.row_req[row]];
+}
+
+// 16-byte unit u of LDS row r lives at unit u ^ (r & 7).
+__device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 7); }
+
+constexpr int kStageBytes = 128;      // K bytes per row per LDS stage
+constexpr int kUnits = kStageBytes / 16;
+
+template <int BM, int BN> struct TileCfg {
+    static constexpr int WM = 2, WN = 2;
+    static constexpr int WTM = BM / WM, WTN = BN / WN;
+    static constexpr int FM = WTM / 32, FN = WTN / 32;
+    static constexpr int LA = BM * kUnits / 256, LB = BN * kUnits / 256;
+    static constexpr int stage_bytes = (BM + BN) * kStageBytes;
+    static_assert(FM >= 1 && FN >= 1 && LA >= 1 && LB >= 1, "tile too small");
+};
+
+template <typename OP, int BM, int BN, int EPI>
+__global__ void __launch_bounds__(256, 1)
+phase_kernel(const ProblemSet set, const PhaseArgs args) {
+    using C = TileCfg<BM, BN>;
+    constexpr int OPB = OpTraits<OP>::bytes;
+    constexpr int KE = kStageBytes / OPB;  // K elements per stage
+    __shared__ __attribute__((aligned(16))) char smem[2 * C::stage_bytes];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / C::WN, wn = wave % C::WN;
+
+    // Energy of the previous error phase, reduced per row in a fixed order
+    // before any tile work (deterministic, no atomics).
+    if (EPI == EPI_UPDATE && args.energy_out != nullptr) {
+        for (int row = blockIdx.x * 256 + tid; row < args.batch; row += gridDim.x * 256) {
+            float s = 0.f;
+            for (int k = 0; k < args.nslots; ++k) s += args.energy_part[(size_t)k * args.ldp + row];
+            args.energy_out[(size_t)args.t * args.batch + row] = s;
+        }
+    }
+
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    // `set` is the first kernel argument, so it sits at offset 0 of the kernarg
+    // segment: index the problems there (scalar loads from constant memory)
+    // instead of letting the compiler copy the whole set to scratch.
+    typedef const __attribute__((address_space(4))) Problem KProblem;
+    KProblem* kprobs = (KProblem*)__builtin_amdgcn_kernarg_segment_ptr();
+    int p = 0;
+    while (p + 1 < set.n && bid >= kprobs[p + 1].tile_start) ++p;
+    const Problem P = load_problem(kprobs + p);
+    int local = bid - P.tile_start;
+    // Grouped order: runs of 8 row tiles share one column tile.
+    const int G = 8;
+    int group = local / (G * P.tiles_n);
+    int first_m = group * G;
+    int gsize = min(P.tiles_m - first_m, G);
+    int in_group = local - group * G * P.tiles_n;
+    const int tm = first_m + in_group % gsize;
+    const int tn = in_group / gsize;
+    const int row0 = tm * BM, col0 = tn * BN;
+
+    if (args.row_req != nullptr) {
+        bool act = false;
+        if (tid < BM) { int r = row0 + tid; act = r < P.M && row_active(args, r); }
+        if (!__syncthreads_or(act)) return;
+    }
+
+    // ---- main loop
+    f32x16 acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x16{};
+
+    typedef const __attribute__((address_space(1))) char GChar;
+    typedef const __attribute__((address_space(1))) u32x4 GVec;
+    GChar* Ag = (GChar*)P.A + (size_t)row0 * P.lda * OPB;
+    GChar* Bg = (GChar*)P.B + (size_t)col0 * P.ldb * OPB;
+    const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
+    const int nk = P.K / KE;
+
+    u32x4 ra[C::LA], rb[C::LB];
+    auto gload = [&](int kt) PCD_INLINE {
+        const size_t kb = (size_t)kt * kStageBytes;
+#pragma unroll
+        for (int i = 0; i < C::LA; ++i) {
+            int u = tid + i * 256, r = u / kUnits, j = u % kUnits;
+            ra[i] = *(GVec*)(Ag + r * lda_b + kb + j * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < C::LB; ++i) {
+            int u = tid + i * 256, r = u / kUnits, j = u % kUnits;
+            rb[i] = *(GVec*)(Bg + r * ldb_b + kb + j * 16);
+        }
+    };
+    auto sstore = [&](int stage) PCD_INLINE {
+        char* sA = smem + stage * C::stage_bytes;
+        char* sB = sA + BM * kStageBytes;
+#pragma unroll
+        for (int i = 0; i < C::LA; ++i) {
+            int u = tid + i * 256, r = u / kUnits, j = u % kUnits;
+            *(u32x4*)(sA + r * kStageBytes + swz(r, j) * 16) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < C::LB; ++i) {
+            int u = tid + i * 256, r = u / kUnits, j = u % kUnits;
+            *(u32x4*)(sB + r * kStageBytes + swz(r, j) * 16) = rb[i];
+        }
+    };
+    auto compute = [&](int stage) PCD_INLINE {
+        const char* sA = smem + stage * C::stage_bytes;
+        const char* sB = sA + BM * kStageBytes;
+        const int half = lane >> 5, lr = lane & 31;
+#pragma unroll
+        for (int c = 0; c < kStageBytes / 32; ++c) {
+            u32x4 a[C::FM], b[C::FN];
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) {
+                int r = wm * C::WTM + i * 32 + lr;
+                a[i] = *(const u32x4*)(sA + r * kStageBytes + swz(r, 2 * c + half) * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) {
+                int r = wn * C::WTN + j * 32 + lr;
+                b[j] = *(const u32x4*)(sB + r * kStageBytes + swz(r, 2 * c + half) * 16);
+            }
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j) mfma_chunk<OP>(acc[i][j], a[i], b[j]);
+        }
+    };
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        if (kt + 1 < nk) gload(kt + 1);
+        compute(kt & 1);
+        if (kt + 1 < nk) sstore((kt + 1) & 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue
+    const int half = lane >> 5, lr = lane & 31;
+    // Row of register r of a block in row-block i: 8*(r/4) + 4*half + r%4.
+    auto row_of = [&](int i, int r) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
+    auto col_of = [&](int j) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + lr; };
+    if constexpr (EPI == EPI_ERROR) {
+        const float P_low = P.prec, inv2p = 0.5f / P.prec;
+        const bool want_energy = args.energy_part != nullptr;
+        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+            constexpr int i = decltype(I)::value;
+            float esum[16];
+            static_for<0, 16>([&](auto R) PCD_INLINE { esum[decltype(R)::value] = 0.f; });
+            static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                constexpr int j = decltype(J)::value;
+                __builtin_amdgcn_sched_barrier(0);  // keep each block's epilogue to itself
+                const int col = col_of(j);
+                const bool cok = col < P.N;
+                const float bj = cok ? P.bias[col] : 0.f;
+                static_for<0, 16>([&](auto R) PCD_INLINE {
+                    constexpr int r = decltype(R)::value;
+                    const int row = row_of(i, r);
+                    if (cok && row < P.M && row_active(args, row)) {
+                        const size_t idx = (size_t)row * P.ldo + col;
+                        const float pre = acc[i][j][r] + bj;
+                        const float y = act_f(args.act, pre);
+                        const float e = P_low * (P.mlow[idx] - y);
+                        const float d = act_df(args.act, pre, y) * e;
+                        OpTraits<OP>::store(P.dout, idx, d);
+                        if (P.eout) P.eout[idx] = e;
+                        esum[r] += e * e * inv2p;
+                    }
+                });
+            });
+            if (want_energy) {
+                static_for<0, 16>([&](auto R) PCD_INLINE {
+                    constexpr int r = decltype(R)::value;
+                    float v = esum[r];
+                    v += __shfl_xor(v, 16);
+                    v += __shfl_xor(v, 8);
+                    v += __shfl_xor(v, 4);
+                    v += __shfl_xor(v, 2);
+                    v += __shfl_xor(v, 1);
+                    esum[r] = v;
+                });
+                if (lr == 0) {
+                    const int slot = P.slot_base + tn * C::WN + wn;
+                    static_for<0, 16>([&](auto R) PCD_INLINE {
+                        constexpr int r = decltype(R)::value;
+                        const int row = row_of(i, r);
+                        if (row < P.M) args.energy_part[(size_t)slot * args.ldp + row] = esum[r];
+                    });
+                }
+            }
+        });
+    } else if constexpr (EPI == EPI_UPDATE) {
+        const float eta = args.eta, lam = args.act_reg;
+        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+            constexpr int i = decltype(I)::value;
+            static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                constexpr int j = decltype(J)::value;
+                __builtin_amdgcn_sched_barrier(0);  // keep each block's epilogue to itself
+                const int col = col_of(j);
+                if (col < P.N) {
+                    static_for<0, 16>([&](auto R) PCD_INLINE {
+                        constexpr int r = decltype(R)::value;
+                        const int row = row_of(i, r);
+                        if (row < P.M && row_active(args, row)) {
+                            const size_t idx = (size_t)row * P.ldo + col;
+                            float m = P.m[idx];
+                            float grad = (P.eself ? P.eself[idx] : 0.f) - acc[i][j][r];
+                            if (lam > 0.f) grad += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
+                            m -= eta * grad;
+                            P.m[idx] = m;
+                            if (P.mop) OpTraits<OP>::store(P.mop, idx, m);
+                        }
+                    });
+                }
+            });
+        });
+    } else if constexpr (EPI == EPI_FFG) {
+        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+            constexpr int i = decltype(I)::value;
+            static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                constexpr int j = decltype(J)::value;
+                __builtin_amdgcn_sched_barrier(0);  // keep each block's epilogue to itself
+                const int col = col_of(j);
+                if (col < P.N) {
+                    const float bj = P.bias[col];
+                    static_for<0, 16>([&](auto R) PCD_INLINE {
+                        constexpr int r = decltype(R)::value;
+                        const int row = row_of(i, r);
+                        if (row < P.M) {
+                            const size_t idx = (size_t)row * P.ldo + col;
+                            const float y = act_f(args.act, acc[i][j][r] + bj);
+                            P.m[idx] = y;
+                            if (P.dout) OpTraits<OP>::store(P.dout, idx, y);
+                        }
+                    });
+                }
+            });
+        });
+    } else {  // EPI_PLAIN: C = alpha acc + beta C
+        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+            constexpr int i = decltype(I)::value;
+            static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                constexpr int j = decltype(J)::value;
+                __builtin_amdgcn_sched_barrier(0);  // keep each block's epilogue to itself
+                const int col = col_of(j);
+                if (col < P.N) {
+                    static_for<0, 16>([&](auto R) PCD_INLINE {
+                        constexpr int r = decltype(R)::value;
+                        const int row = row_of(i, r);
+                        if (row < P.M) {
+                            const size_t idx = (size_t)row * P.ldo + col;
+                            float v = args.alpha * acc[i][j][r];
+                            if (args.beta != 0.f) v += args.beta * P.m[idx];
+                            P.m[idx] = v;
+                        }
+                    });
+                }
+            });
+        });
+    }
+}
+
+// ------------------------------------------------------------ small kernels
+
+// Zero-fill of n 16-byte units (used inside captured graphs instead of
+// hipMemsetAsync).
+__global__ void zero_kernel(u32x4* __restrict__ p, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// Pack a row-major [rows x cols] fp32 matrix (optionally read transposed) into
+// a zero-padded [prow x pcol] buffer of the operand type.
+template <typename OP>
+__global__ void pack_kernel(const void* __restrict__ src, int src_is_f32, int rows, int cols, int trans,
+                            void* __restrict__ dst, int prow, int pcol) {
+    size_t n = (size_t)prow * pcol;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        int r = (int)(i / pcol), c = (int)(i % pcol);
+        float v = 0.f;
+        bool inside = r < rows && c < cols;
+        if (inside) {
+            // logical element (r, c) of op(src); physical src is [rows x cols] or [cols x rows]
+            size_t s = trans ? (size_t)c * rows + r : (size_t)r * cols + c;
+            if (src_is_f32) {
+                v = ((const float*)src)[s];
+            } else {
+                // 16-bit source of the operand's own type: copy the bits
+                ((uint16_t*)dst)[i] = ((const uint16_t*)src)[s];
+                continue;
+            }
+        }
+        if (!inside && !src_is_f32) { ((uint16_t*)dst)[i] = 0; continue; }
+        OpTraits<OP>::store(dst, i, v);
+    }
+}
+
+// Ragged early exit, one workgroup per request, between the error and the
+// update phase of step t: sums the request's row energies, records them and
+// decides whether step t is its last (Network.cs:895-905).
+__global__ void exit_kernel(const float* __restrict__ part, int ldp, int nslots, const int* __restrict__ row_offsets,
+                            int* __restrict__ done_at, float* __restrict__ prev_energy, float* __restrict__ last_energy,
+                            int t, int rule, float thr) {
+    const int r = blockIdx.x;
+    if (t >= done_at[r]) return;  // uniform over the workgroup
+    const int r0 = row_offsets[r], r1 = row_offsets[r + 1];
+    float s = 0.f;
+    for (int row = r0 + threadIdx.x; row < r1; row += blockDim.x)
+        for (int k = 0; k < nslots; ++k) s += part[(size_t)k * ldp + row];
+    __shared__ float red[256];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const float e = red[0];
+        const float prev = prev_energy[r];
+        bool stop = false;
+        if (rule == 1) stop = thr > 0.f && t > 0 && (prev - e < thr * fmaxf(prev, 1e-12f));
+        else if (rule == 2) stop = e / (float)(r1 - r0) < thr;
+        last_energy[r] = e;
+        prev_energy[r] = e;
+        if (stop) done_at[r] = t + 1;
+    }
+}
+
+}  // namespace pcd

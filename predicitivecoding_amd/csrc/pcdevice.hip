@@ -1,0 +1,1075 @@
+// pcdevice.hip -- C ABI of libpcdevice_hip (declared in include/pcdevice.h).
+//
+// Host side of the MI355X relaxation: the device runtime calls the reference
+// binds through P/Invoke (PredictiveCoding.Device/Interop/*.cs), a pooled
+// allocator (Allocators/CudaAllocator.cs), streams and events
+// (Streams/CudaStreamManager.cs), row-major GEMMs (Gemm/CudaGemmProvider.cs)
+// and the batched relaxation itself (BatchedPcForward.cs) with its ragged,
+// early-exit variant (Network.cs:760-907 applied per request).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/pcdevice.h"
+#include "pc_kernels.hpp"
+
+using namespace pcd;
+
+namespace {
+
+// ------------------------------------------------------------------ errors
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int from_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return PCD_SUCCESS;
+    int st = PCD_HIP_ERROR;
+    if (e == hipErrorNoDevice) st = PCD_NO_DEVICE;
+    else if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) st = PCD_OUT_OF_MEMORY;
+    else if (e == hipErrorInvalidValue || e == hipErrorInvalidDevicePointer || e == hipErrorInvalidDevice)
+        st = PCD_INVALID_VALUE;
+    else if (e == hipErrorNotSupported) st = PCD_NOT_SUPPORTED;
+    return fail(st, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+#define HIP_TRY(call)                                    \
+    do {                                                 \
+        hipError_t e_ = (call);                          \
+        if (e_ != hipSuccess) return from_hip(e_, #call); \
+    } while (0)
+
+inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+// --------------------------------------------------------------- allocator
+
+// Power-of-two buckets of at most 32 cached blocks per (device, stream), as
+// CudaAllocator does (CudaAllocator.cs:32-59,98-103).  A block freed on a
+// stream is handed out again only on that stream, so stream order alone keeps
+// a reused block from racing with work still queued on it.
+struct Pool {
+    std::mutex mu;
+    struct Key {
+        int dev;
+        void* stream;
+        int bucket;
+        bool operator<(const Key& o) const {
+            if (dev != o.dev) return dev < o.dev;
+            if (stream != o.stream) return stream < o.stream;
+            return bucket < o.bucket;
+        }
+    };
+    std::map<Key, std::vector<void*>> free_blocks;
+    std::unordered_map<void*, std::pair<int, int>> live;  // ptr -> (device, bucket)
+    std::map<int, std::vector<void*>> host_free;          // bucket -> pinned blocks
+    std::unordered_map<void*, int> host_live;
+    static constexpr size_t kMaxCached = 32;
+};
+Pool& pool() {
+    static Pool* p = new Pool();  // leaked on purpose: outlives static destructors
+    return *p;
+}
+
+int bucket_of(size_t bytes) {
+    int b = 8;  // 256 B minimum
+    while (((size_t)1 << b) < bytes) ++b;
+    return b;
+}
+
+int pool_alloc(void** out, size_t bytes, hipStream_t stream) {
+    if (!out) return fail(PCD_INVALID_VALUE, "pcd_malloc_async: null out pointer");
+    *out = nullptr;
+    if (bytes == 0) return PCD_SUCCESS;
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    int b = bucket_of(bytes);
+    Pool& P = pool();
+    {
+        std::lock_guard<std::mutex> g(P.mu);
+        auto it = P.free_blocks.find({dev, (void*)stream, b});
+        if (it != P.free_blocks.end() && !it->second.empty()) {
+            *out = it->second.back();
+            it->second.pop_back();
+            P.live[*out] = {dev, b};
+            return PCD_SUCCESS;
+        }
+    }
+    void* p = nullptr;
+    hipError_t e = hipMallocAsync(&p, (size_t)1 << b, stream);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        e = hipMalloc(&p, (size_t)1 << b);  // CudaAllocator.cs:43-44 fallback
+    }
+    if (e != hipSuccess) return from_hip(e, "pcd_malloc_async");
+    std::lock_guard<std::mutex> g(P.mu);
+    P.live[p] = {dev, b};
+    *out = p;
+    return PCD_SUCCESS;
+}
+
+int pool_free(void* ptr, hipStream_t stream) {
+    if (!ptr) return PCD_SUCCESS;
+    Pool& P = pool();
+    std::lock_guard<std::mutex> g(P.mu);
+    auto it = P.live.find(ptr);
+    if (it == P.live.end()) return fail(PCD_INVALID_VALUE, "pcd_free_async: pointer not from pcd_malloc_async");
+    auto [dev, b] = it->second;
+    P.live.erase(it);
+    auto& v = P.free_blocks[{dev, (void*)stream, b}];
+    if (v.size() < Pool::kMaxCached) {
+        v.push_back(ptr);
+        return PCD_SUCCESS;
+    }
+    HIP_TRY(hipFreeAsync(ptr, stream));
+    return PCD_SUCCESS;
+}
+
+// ------------------------------------------------------------------ launch
+
+template <typename OP, int BM, int BN>
+int launch_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
+    switch (epi) {
+    case EPI_ERROR: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_ERROR>), dim3(grid), dim3(256), 0, s, set, args); break;
+    case EPI_UPDATE: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_UPDATE>), dim3(grid), dim3(256), 0, s, set, args); break;
+    case EPI_FFG: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_FFG>), dim3(grid), dim3(256), 0, s, set, args); break;
+    default: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN>), dim3(grid), dim3(256), 0, s, set, args); break;
+    }
+    return from_hip(hipGetLastError(), "phase_kernel launch");
+}
+
+template <typename OP>
+int launch_op(int tile, int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
+    switch (tile) {
+    case 64: return launch_tile<OP, 64, 64>(epi, set, args, grid, s);
+    case 128: return launch_tile<OP, 128, 128>(epi, set, args, grid, s);
+    case 256: return launch_tile<OP, 256, 256>(epi, set, args, grid, s);
+    default: return fail(PCD_INVALID_VALUE, "unsupported tile %d", tile);
+    }
+}
+
+int launch_phase(int dtype, int tile, int epi, const ProblemSet& set, const PhaseArgs& args, hipStream_t s) {
+    int grid = 0;
+    for (int i = 0; i < set.n; ++i) grid += set.p[i].tiles_m * set.p[i].tiles_n;
+    if (grid == 0) return PCD_SUCCESS;
+    switch (dtype) {
+    case PCD_F32: return launch_op<float>(tile, epi, set, args, grid, s);
+    case PCD_BF16: return launch_op<bf16_t>(tile, epi, set, args, grid, s);
+    case PCD_F16: return launch_op<f16_t>(tile, epi, set, args, grid, s);
+    default: return fail(PCD_INVALID_VALUE, "unknown dtype %d", dtype);
+    }
+}
+
+int launch_zero(void* p, size_t bytes, hipStream_t s) {
+    size_t units = bytes / 16;
+    if (units == 0) return PCD_SUCCESS;
+    int grid = (int)std::min<size_t>((units + 255) / 256, 4096);
+    hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(256), 0, s, (u32x4*)p, units);
+    return from_hip(hipGetLastError(), "zero_kernel launch");
+}
+
+inline int op_bytes(int dtype) { return dtype == PCD_F32 ? 4 : 2; }
+
+// --------------------------------------------------------------- PC model
+
+constexpr int kFeatPad = 64;    // feature dims padded to the deepest LDS stage (64 elements)
+constexpr int kRowPad = 256;    // row dims padded to the widest tile
+
+struct Plan;
+
+// Per (model, stream) device buffers for batches up to `cap` rows.
+struct Workspace {
+    hipStream_t stream = nullptr;
+    int cap = 0;                       // rows, multiple of kRowPad
+    std::vector<float*> M;             // [L] fp32 states (M[0] = clamped input)
+    std::vector<void*> S;              // [L] operand-type state copies (16-bit dtypes only)
+    std::vector<void*> D;              // [L] D_l, l >= 1, operand type [cap x P_{l-1}]
+    std::vector<float*> E;             // [L] E_l, 1 <= l <= L-2, fp32 [cap x P_l]
+    float* energy_part = nullptr;      // [slots x cap]
+    int slots_cap = 0;
+    hipStream_t capture = nullptr;     // private stream used for graph capture
+    std::vector<std::unique_ptr<Plan>> plans;
+    std::vector<void*> owned;          // every hipMalloc'ed buffer
+};
+
+struct Plan {
+    int batch = 0, steps = 0, want_energy = 0, tile = 0, ffg = 0;
+    float* energy_out = nullptr;       // [steps x batch]
+    hipGraphExec_t exec = nullptr;
+    hipGraph_t graph = nullptr;
+    uint64_t last_use = 0;
+};
+
+}  // namespace
+
+struct pcd_model {
+    int device = 0;
+    int L = 0;
+    std::vector<int> s, P;              // sizes, padded sizes
+    int act = 0, ffg = 0, dtype = 0;
+    float eta = 0.f, act_reg = 0.f;
+    std::vector<float> prec;
+    std::vector<void*> W, WT;           // [L] operand type; W[l] is [R(s_{l-1}) x P_l], WT[l] [R(s_l) x P_{l-1}]
+    std::vector<float*> bias;           // [L] fp32 [P_{l-1}]
+    std::mutex mu;
+    std::vector<std::unique_ptr<Workspace>> ws;
+    // options
+    int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0;
+    float prof_err_ms = 0.f, prof_upd_ms = 0.f;
+    int prof_launches = 0;
+    uint64_t clock = 0;
+};
+
+namespace {
+
+void free_workspace(Workspace& w) {
+    for (auto& p : w.plans) {
+        if (p->exec) (void)hipGraphExecDestroy(p->exec);
+        if (p->graph) (void)hipGraphDestroy(p->graph);
+        if (p->energy_out) (void)hipFree(p->energy_out);
+    }
+    w.plans.clear();
+    for (void* p : w.owned) (void)hipFree(p);
+    w.owned.clear();
+    if (w.capture) (void)hipStreamDestroy(w.capture);
+    w.capture = nullptr;
+}
+
+int dev_alloc_zero(std::vector<void*>& owned, void** out, size_t bytes) {
+    *out = nullptr;
+    if (bytes == 0) return PCD_SUCCESS;
+    HIP_TRY(hipMalloc(out, bytes));
+    owned.push_back(*out);
+    HIP_TRY(hipMemset(*out, 0, bytes));
+    return PCD_SUCCESS;
+}
+
+int choose_tile(const pcd_model* m, int batch) {
+    if (m->tile_m > 0) return m->tile_m;
+    if (batch <= 64) return 64;
+    if (m->dtype != PCD_F32 && batch >= 1024) {
+        bool wide = true;
+        for (int l = 0; l < m->L; ++l) wide = wide && m->s[l] >= 1024;
+        if (wide) return 256;
+    }
+    return 128;
+}
+
+int energy_slots(const pcd_model* m, int tile) {
+    int slots = 0;
+    for (int l = 1; l < m->L; ++l) slots += (int)((m->s[l - 1] + tile - 1) / tile) * 2;
+    return slots;
+}
+
+int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out) {
+    Workspace* w = nullptr;
+    for (auto& x : m->ws)
+        if (x->stream == stream) w = x.get();
+    if (!w) {
+        m->ws.emplace_back(new Workspace());
+        w = m->ws.back().get();
+        w->stream = stream;
+    }
+    int need = (int)round_up((size_t)std::max(rows, 1), kRowPad);
+    int slots = energy_slots(m, 64);  // the smallest tile has the most slots
+    if (w->cap >= need && w->slots_cap >= slots) {
+        *out = w;
+        return PCD_SUCCESS;
+    }
+    HIP_TRY(hipStreamSynchronize(stream));
+    free_workspace(*w);
+    const int L = m->L, ob = op_bytes(m->dtype);
+    w->cap = need;
+    w->M.assign(L, nullptr);
+    w->S.assign(L, nullptr);
+    w->D.assign(L, nullptr);
+    w->E.assign(L, nullptr);
+    int st;
+    for (int l = 0; l < L; ++l) {
+        if ((st = dev_alloc_zero(w->owned, (void**)&w->M[l], (size_t)need * m->P[l] * 4))) return st;
+        if (l >= 1 && m->dtype != PCD_F32)
+            if ((st = dev_alloc_zero(w->owned, &w->S[l], (size_t)need * m->P[l] * ob))) return st;
+        if (l >= 1)
+            if ((st = dev_alloc_zero(w->owned, &w->D[l], (size_t)need * m->P[l - 1] * ob))) return st;
+        if (l >= 1 && l <= L - 2)
+            if ((st = dev_alloc_zero(w->owned, (void**)&w->E[l], (size_t)need * m->P[l] * 4))) return st;
+    }
+    w->slots_cap = slots;
+    if ((st = dev_alloc_zero(w->owned, (void**)&w->energy_part, (size_t)slots * need * 4))) return st;
+    HIP_TRY(hipStreamCreateWithFlags(&w->capture, hipStreamNonBlocking));
+    *out = w;
+    return PCD_SUCCESS;
+}
+
+// Operand of the error-phase GEMM for layer l: the fp32 state itself, or its
+// 16-bit copy.
+const void* state_operand(const pcd_model* m, const Workspace* w, int l) {
+    return m->dtype == PCD_F32 ? (const void*)w->M[l] : w->S[l];
+}
+
+// Problem sets of the two phases for a batch; problems beyond kMaxProblems
+// spill into further sets (still one phase: the problems are independent).
+void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, int tile, int ragged,
+                      std::vector<ProblemSet>& err, std::vector<ProblemSet>& upd, int* nslots) {
+    err.clear();
+    upd.clear();
+    const int L = m->L;
+    const int tm = (batch + tile - 1) / tile;
+    int slot = 0;
+    for (int l = L - 1; l >= 1; --l) {   // error phase: widest K first is irrelevant; keep layer order
+        if (err.empty() || err.back().n == kMaxProblems) { err.emplace_back(); err.back().n = 0; }
+        ProblemSet& ps = err.back();
+        int start = ps.n ? ps.p[ps.n - 1].tile_start + ps.p[ps.n - 1].tiles_m * ps.p[ps.n - 1].tiles_n : 0;
+        Problem& p = ps.p[ps.n++];
+        std::memset(&p, 0, sizeof p);
+        p.A = state_operand(m, w, l);
+        p.lda = m->P[l];
+        p.B = m->W[l];
+        p.ldb = m->P[l];
+        p.M = batch;
+        p.N = m->s[l - 1];
+        p.K = m->P[l];
+        p.tiles_m = tm;
+        p.tiles_n = (p.N + tile - 1) / tile;
+        p.tile_start = start;
+        p.ldo = m->P[l - 1];
+        p.bias = m->bias[l];
+        p.mlow = w->M[l - 1];
+        p.eout = l - 1 >= 1 ? w->E[l - 1] : nullptr;
+        p.dout = w->D[l];
+        p.prec = m->prec[l - 1];
+        p.slot_base = slot;
+        slot += p.tiles_n * 2;
+    }
+    for (int l = 1; l < L; ++l) {
+        if (upd.empty() || upd.back().n == kMaxProblems) { upd.emplace_back(); upd.back().n = 0; }
+        ProblemSet& ps = upd.back();
+        int start = ps.n ? ps.p[ps.n - 1].tile_start + ps.p[ps.n - 1].tiles_m * ps.p[ps.n - 1].tiles_n : 0;
+        Problem& p = ps.p[ps.n++];
+        std::memset(&p, 0, sizeof p);
+        p.A = w->D[l];
+        p.lda = m->P[l - 1];
+        p.B = m->WT[l];
+        p.ldb = m->P[l - 1];
+        p.M = batch;
+        p.N = m->s[l];
+        p.K = m->P[l - 1];
+        p.tiles_m = tm;
+        p.tiles_n = (p.N + tile - 1) / tile;
+        p.tile_start = start;
+        p.ldo = m->P[l];
+        p.m = w->M[l];
+        p.mop = m->dtype == PCD_F32 ? nullptr : w->S[l];
+        p.eself = l <= L - 2 ? w->E[l] : nullptr;
+    }
+    (void)ragged;
+    *nslots = slot;
+}
+
+PhaseArgs base_args(const pcd_model* m, const Workspace* w, int batch, int nslots) {
+    PhaseArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.act = m->act;
+    a.eta = m->eta;
+    a.act_reg = m->act_reg;
+    a.alpha = 1.f;
+    a.energy_part = w->energy_part;
+    a.ldp = w->cap;
+    a.nslots = nslots;
+    a.batch = batch;
+    return a;
+}
+
+// Zero the free states, FFG warm start (Network.cs:121-131), then the step loop.
+// With `events` set, each phase launch is bracketed by HIP events (eager only).
+struct PhaseTimer {
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> err, upd;
+};
+
+int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, int tile, float* energy_out,
+                  const int* row_req, int* done_at, const int* row_offsets_dev, int requests, int exit_rule,
+                  float exit_thr, float* prev_energy, float* last_energy, hipStream_t s, PhaseTimer* timer) {
+    const int L = m->L;
+    int st;
+    for (int l = 1; l < L; ++l) {
+        if ((st = launch_zero(w->M[l], (size_t)w->cap * m->P[l] * 4, s))) return st;
+        if (w->S[l] && (st = launch_zero(w->S[l], (size_t)w->cap * m->P[l] * op_bytes(m->dtype), s))) return st;
+    }
+    std::vector<ProblemSet> err, upd;
+    int nslots = 0;
+    build_phase_sets(m, w, batch, tile, row_req != nullptr, err, upd, &nslots);
+    PhaseArgs args = base_args(m, w, batch, nslots);
+    args.row_req = row_req;
+    args.done_at = done_at;
+    const bool need_energy = energy_out != nullptr || row_req != nullptr;
+    if (!need_energy) args.energy_part = nullptr;
+
+    if (m->ffg) {
+        for (int l = L - 1; l >= 2; --l) {
+            ProblemSet ps;
+            std::memset(&ps, 0, sizeof ps);
+            ps.n = 1;
+            Problem& p = ps.p[0];
+            p.A = state_operand(m, w, l);
+            p.lda = m->P[l];
+            p.B = m->W[l];
+            p.ldb = m->P[l];
+            p.M = batch;
+            p.N = m->s[l - 1];
+            p.K = m->P[l];
+            p.tiles_m = (batch + tile - 1) / tile;
+            p.tiles_n = (p.N + tile - 1) / tile;
+            p.ldo = m->P[l - 1];
+            p.bias = m->bias[l];
+            p.m = w->M[l - 1];
+            p.dout = m->dtype == PCD_F32 ? nullptr : w->S[l - 1];
+            PhaseArgs fa = args;
+            fa.row_req = nullptr;
+            if ((st = launch_phase(m->dtype, tile, EPI_FFG, ps, fa, s))) return st;
+        }
+    }
+    for (int t = 0; t < steps; ++t) {
+        PhaseArgs a = args;
+        a.t = t;
+        a.energy_out = nullptr;
+        hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+        if (timer) {
+            HIP_TRY(hipEventCreate(&e0));
+            HIP_TRY(hipEventCreate(&e1));
+            HIP_TRY(hipEventCreate(&e2));
+            HIP_TRY(hipEventRecord(e0, s));
+        }
+        for (auto& ps : err)
+            if ((st = launch_phase(m->dtype, tile, EPI_ERROR, ps, a, s))) return st;
+        if (timer) HIP_TRY(hipEventRecord(e1, s));
+        if (row_req) {
+            hipLaunchKernelGGL(exit_kernel, dim3(requests), dim3(256), 0, s, (const float*)w->energy_part, w->cap,
+                               nslots, row_offsets_dev, done_at, prev_energy, last_energy, t, exit_rule, exit_thr);
+            if ((st = from_hip(hipGetLastError(), "exit_kernel launch"))) return st;
+        }
+        a.energy_out = energy_out;
+        bool first = true;
+        for (auto& ps : upd) {
+            PhaseArgs ua = a;
+            if (!first) ua.energy_out = nullptr;
+            first = false;
+            if ((st = launch_phase(m->dtype, tile, EPI_UPDATE, ps, ua, s))) return st;
+        }
+        if (timer) {
+            HIP_TRY(hipEventRecord(e2, s));
+            timer->err.push_back({e0, e1});
+            timer->upd.push_back({e1, e2});
+        }
+    }
+    return PCD_SUCCESS;
+}
+
+Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy, int tile, int* status) {
+    *status = PCD_SUCCESS;
+    for (auto& p : w->plans)
+        if (p->batch == batch && p->steps == steps && p->want_energy == want_energy && p->tile == tile) {
+            p->last_use = ++m->clock;
+            return p.get();
+        }
+    if (w->plans.size() >= 8) {  // evict the least recently used plan
+        auto it = std::min_element(w->plans.begin(), w->plans.end(),
+                                   [](const auto& a, const auto& b) { return a->last_use < b->last_use; });
+        if ((*it)->exec) (void)hipGraphExecDestroy((*it)->exec);
+        if ((*it)->graph) (void)hipGraphDestroy((*it)->graph);
+        if ((*it)->energy_out) (void)hipFree((*it)->energy_out);
+        w->plans.erase(it);
+    }
+    std::unique_ptr<Plan> p(new Plan());
+    p->batch = batch;
+    p->steps = steps;
+    p->want_energy = want_energy;
+    p->tile = tile;
+    p->last_use = ++m->clock;
+    if (want_energy) {
+        hipError_t e = hipMalloc(&p->energy_out, (size_t)steps * batch * 4);
+        if (e != hipSuccess) { *status = from_hip(e, "hipMalloc(energy)"); return nullptr; }
+    }
+    if (m->use_graph) {
+        hipStream_t cs = w->capture;
+        hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) { *status = from_hip(e, "hipStreamBeginCapture"); return nullptr; }
+        int st = enqueue_relax(m, w, batch, steps, tile, p->energy_out, nullptr, nullptr, nullptr, 0, 0, 0.f,
+                               nullptr, nullptr, cs, nullptr);
+        hipGraph_t g = nullptr;
+        e = hipStreamEndCapture(cs, &g);
+        if (st) { if (g) (void)hipGraphDestroy(g); *status = st; return nullptr; }
+        if (e != hipSuccess) { *status = from_hip(e, "hipStreamEndCapture"); return nullptr; }
+        p->graph = g;
+        e = hipGraphInstantiate(&p->exec, g, nullptr, nullptr, 0);
+        if (e != hipSuccess) { *status = from_hip(e, "hipGraphInstantiate"); return nullptr; }
+    }
+    w->plans.push_back(std::move(p));
+    return w->plans.back().get();
+}
+
+int check_model(pcd_model* m) {
+    if (!m) return fail(PCD_NOT_INITIALIZED, "null model");
+    return PCD_SUCCESS;
+}
+
+}  // namespace
+
+// ======================================================================= ABI
+
+extern "C" {
+
+int pcd_version(int* version) {
+    if (!version) return fail(PCD_INVALID_VALUE, "null pointer");
+    *version = 100;  // 0.1.0
+    return PCD_SUCCESS;
+}
+
+int pcd_last_error(char* buf, size_t len) {
+    if (!buf || len == 0) return fail(PCD_INVALID_VALUE, "pcd_last_error: empty buffer");
+    std::snprintf(buf, len, "%s", g_last_error.c_str());
+    return PCD_SUCCESS;
+}
+
+int pcd_get_device_count(int* count) {
+    if (!count) return fail(PCD_INVALID_VALUE, "pcd_get_device_count: null pointer");
+    *count = 0;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(PCD_NO_DEVICE, "no HIP device (%s)", hipGetErrorString(e));
+    }
+    *count = n;
+    return n > 0 ? PCD_SUCCESS : fail(PCD_NO_DEVICE, "no HIP device");
+}
+
+int pcd_set_device(int device) {
+    HIP_TRY(hipSetDevice(device));
+    return PCD_SUCCESS;
+}
+
+int pcd_get_device(int* device) {
+    if (!device) return fail(PCD_INVALID_VALUE, "null pointer");
+    HIP_TRY(hipGetDevice(device));
+    return PCD_SUCCESS;
+}
+
+int pcd_device_synchronize(void) {
+    HIP_TRY(hipDeviceSynchronize());
+    return PCD_SUCCESS;
+}
+
+// ----------------------------------------------------------------- memory
+
+int pcd_malloc_async(void** ptr, size_t bytes, void* stream) { return pool_alloc(ptr, bytes, (hipStream_t)stream); }
+
+int pcd_free_async(void* ptr, void* stream) { return pool_free(ptr, (hipStream_t)stream); }
+
+int pcd_host_alloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(PCD_INVALID_VALUE, "pcd_host_alloc: null out pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return PCD_SUCCESS;
+    int b = bucket_of(bytes);
+    Pool& P = pool();
+    {
+        std::lock_guard<std::mutex> g(P.mu);
+        auto& v = P.host_free[b];
+        if (!v.empty()) {
+            *ptr = v.back();
+            v.pop_back();
+            P.host_live[*ptr] = b;
+            return PCD_SUCCESS;
+        }
+    }
+    void* p = nullptr;
+    HIP_TRY(hipHostMalloc(&p, (size_t)1 << b, hipHostMallocDefault));
+    std::lock_guard<std::mutex> g(P.mu);
+    P.host_live[p] = b;
+    *ptr = p;
+    return PCD_SUCCESS;
+}
+
+int pcd_host_free(void* ptr) {
+    if (!ptr) return PCD_SUCCESS;
+    Pool& P = pool();
+    std::lock_guard<std::mutex> g(P.mu);
+    auto it = P.host_live.find(ptr);
+    if (it == P.host_live.end()) return fail(PCD_INVALID_VALUE, "pcd_host_free: pointer not from pcd_host_alloc");
+    int b = it->second;
+    P.host_live.erase(it);
+    auto& v = P.host_free[b];
+    if (v.size() < Pool::kMaxCached) {
+        v.push_back(ptr);
+        return PCD_SUCCESS;
+    }
+    HIP_TRY(hipHostFree(ptr));
+    return PCD_SUCCESS;
+}
+
+int pcd_trim_pools(void) {
+    HIP_TRY(hipDeviceSynchronize());
+    Pool& P = pool();
+    std::lock_guard<std::mutex> g(P.mu);
+    for (auto& kv : P.free_blocks)
+        for (void* p : kv.second) (void)hipFree(p);
+    P.free_blocks.clear();
+    for (auto& kv : P.host_free)
+        for (void* p : kv.second) (void)hipHostFree(p);
+    P.host_free.clear();
+    return PCD_SUCCESS;
+}
+
+static int to_kind(int kind, hipMemcpyKind* out) {
+    switch (kind) {
+    case PCD_HOST_TO_HOST: *out = hipMemcpyHostToHost; return PCD_SUCCESS;
+    case PCD_HOST_TO_DEVICE: *out = hipMemcpyHostToDevice; return PCD_SUCCESS;
+    case PCD_DEVICE_TO_HOST: *out = hipMemcpyDeviceToHost; return PCD_SUCCESS;
+    case PCD_DEVICE_TO_DEVICE: *out = hipMemcpyDeviceToDevice; return PCD_SUCCESS;
+    case PCD_MEMCPY_DEFAULT: *out = hipMemcpyDefault; return PCD_SUCCESS;
+    default: return fail(PCD_INVALID_VALUE, "bad memcpy kind %d", kind);
+    }
+}
+
+int pcd_memcpy(void* dst, const void* src, size_t bytes, int kind) {
+    hipMemcpyKind k;
+    if (int st = to_kind(kind, &k)) return st;
+    if (bytes == 0) return PCD_SUCCESS;
+    if (!dst || !src) return fail(PCD_INVALID_VALUE, "pcd_memcpy: null pointer");
+    HIP_TRY(hipMemcpy(dst, src, bytes, k));
+    return PCD_SUCCESS;
+}
+
+int pcd_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream) {
+    hipMemcpyKind k;
+    if (int st = to_kind(kind, &k)) return st;
+    if (bytes == 0) return PCD_SUCCESS;
+    if (!dst || !src) return fail(PCD_INVALID_VALUE, "pcd_memcpy_async: null pointer");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, k, (hipStream_t)stream));
+    return PCD_SUCCESS;
+}
+
+int pcd_memset_async(void* dst, int value, size_t bytes, void* stream) {
+    if (bytes == 0) return PCD_SUCCESS;
+    if (!dst) return fail(PCD_INVALID_VALUE, "pcd_memset_async: null pointer");
+    HIP_TRY(hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
+    return PCD_SUCCESS;
+}
+
+// ---------------------------------------------------------- streams, events
+
+int pcd_stream_create(void** stream) {
+    if (!stream) return fail(PCD_INVALID_VALUE, "null pointer");
+    hipStream_t s = nullptr;
+    HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return PCD_SUCCESS;
+}
+
+int pcd_stream_destroy(void* stream) {
+    if (!stream) return PCD_SUCCESS;
+    HIP_TRY(hipStreamDestroy((hipStream_t)stream));
+    return PCD_SUCCESS;
+}
+
+int pcd_stream_synchronize(void* stream) {
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return PCD_SUCCESS;
+}
+
+int pcd_event_create(void** event) {
+    if (!event) return fail(PCD_INVALID_VALUE, "null pointer");
+    hipEvent_t e = nullptr;
+    HIP_TRY(hipEventCreate(&e));
+    *event = e;
+    return PCD_SUCCESS;
+}
+
+int pcd_event_record(void* event, void* stream) {
+    if (!event) return fail(PCD_INVALID_VALUE, "null event");
+    HIP_TRY(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+    return PCD_SUCCESS;
+}
+
+int pcd_event_synchronize(void* event) {
+    if (!event) return PCD_SUCCESS;
+    HIP_TRY(hipEventSynchronize((hipEvent_t)event));
+    return PCD_SUCCESS;
+}
+
+int pcd_event_destroy(void* event) {
+    if (!event) return PCD_SUCCESS;
+    HIP_TRY(hipEventDestroy((hipEvent_t)event));
+    return PCD_SUCCESS;
+}
+
+int pcd_event_elapsed_ms(float* ms, void* start, void* end) {
+    if (!ms || !start || !end) return fail(PCD_INVALID_VALUE, "null pointer");
+    HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+    return PCD_SUCCESS;
+}
+
+// -------------------------------------------------------------------- GEMM
+
+static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int m, int k, int n, int trans_a,
+                       int trans_b, float beta, void* stream_) {
+    if (!dA || !dB || !dC) return fail(PCD_INVALID_VALUE, "pcd_gemm: null pointer");
+    if (m < 1 || k < 1 || n < 1) return fail(PCD_INVALID_VALUE, "pcd_gemm: bad shape %d x %d x %d", m, k, n);
+    hipStream_t s = (hipStream_t)stream_;
+    const int tile = (m <= 64 || n <= 64) ? 64 : 128;
+    const int mp = (int)round_up(m, tile), np = (int)round_up(n, tile), kp = (int)round_up(k, kFeatPad);
+    const int ob = op_bytes(dtype);
+    void *pa = nullptr, *pb = nullptr;
+    int st;
+    if ((st = pool_alloc(&pa, (size_t)mp * kp * ob, s))) return st;
+    if ((st = pool_alloc(&pb, (size_t)np * kp * ob, s))) { pool_free(pa, s); return st; }
+    const int src_f32 = dtype == PCD_F32;
+    auto pack = [&](const void* src, int rows, int cols, int trans, void* dst, int prow, int pcol) -> int {
+        int grid = (int)std::min<size_t>(((size_t)prow * pcol + 255) / 256, 8192);
+        switch (dtype) {
+        case PCD_F32: hipLaunchKernelGGL(pack_kernel<float>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol); break;
+        case PCD_BF16: hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol); break;
+        default: hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol); break;
+        }
+        return from_hip(hipGetLastError(), "pack_kernel launch");
+    };
+    // op(A) [m x k]: physical [m x k], or [k x m] when transposed.
+    // The kernel's B operand is op(B)^T [n x k]: physical B is [k x n] (read
+    // transposed) or, with trans_b, already [n x k].
+    if ((st = pack(dA, m, k, trans_a, pa, mp, kp)) || (st = pack(dB, n, k, trans_b ? 0 : 1, pb, np, kp))) {
+        pool_free(pa, s);
+        pool_free(pb, s);
+        return st;
+    }
+    ProblemSet ps;
+    std::memset(&ps, 0, sizeof ps);
+    ps.n = 1;
+    Problem& p = ps.p[0];
+    p.A = pa;
+    p.lda = kp;
+    p.B = pb;
+    p.ldb = kp;
+    p.M = m;
+    p.N = n;
+    p.K = kp;
+    p.tiles_m = mp / tile;
+    p.tiles_n = np / tile;
+    p.ldo = n;
+    p.m = dC;
+    PhaseArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.alpha = 1.f;
+    a.beta = beta;
+    st = launch_phase(dtype, tile, EPI_PLAIN, ps, a, s);
+    int st2 = pool_free(pa, s);
+    int st3 = pool_free(pb, s);
+    if (st) return st;
+    if (st2) return st2;
+    if (st3) return fail(PCD_GEMM_ERROR, "pcd_gemm: scratch release failed");
+    return PCD_SUCCESS;
+}
+
+int pcd_gemm_f32(const float* dA, const float* dB, float* dC, int m, int k, int n, int trans_a, int trans_b,
+                 float beta, void* stream) {
+    return gemm_common(PCD_F32, dA, dB, dC, m, k, n, trans_a, trans_b, beta, stream);
+}
+
+int pcd_gemm_bf16(const uint16_t* dA, const uint16_t* dB, float* dC, int m, int k, int n, int trans_a, int trans_b,
+                  float beta, void* stream) {
+    return gemm_common(PCD_BF16, dA, dB, dC, m, k, n, trans_a, trans_b, beta, stream);
+}
+
+int pcd_gemm_f16(const uint16_t* dA, const uint16_t* dB, float* dC, int m, int k, int n, int trans_a, int trans_b,
+                 float beta, void* stream) {
+    return gemm_common(PCD_F16, dA, dB, dC, m, k, n, trans_a, trans_b, beta, stream);
+}
+
+// ---------------------------------------------------------------- PC model
+
+int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta, float act_reg, int ffg,
+                        const float* const* W, const float* const* b, const float* precisions, int dtype,
+                        pcd_model** out) {
+    if (!out) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: null out pointer");
+    *out = nullptr;
+    if (!sizes || !W || !b || !precisions) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: null pointer");
+    if (levels < 2) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: need at least 2 levels, got %d", levels);
+    if (activation < PCD_ACT_LINEAR || activation > PCD_ACT_GELU)
+        return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: unknown activation %d", activation);
+    if (dtype != PCD_F32 && dtype != PCD_BF16 && dtype != PCD_F16)
+        return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: unknown dtype %d", dtype);
+    if (!(eta == eta) || !(act_reg >= 0.f)) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: bad eta/act_reg");
+    for (int l = 0; l < levels; ++l) {
+        if (sizes[l] < 1) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: sizes[%d] = %d", l, sizes[l]);
+        if (!(precisions[l] > 0.f)) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: precision[%d] <= 0", l);
+    }
+    for (int l = 1; l < levels; ++l)
+        if (!W[l - 1] || !b[l - 1]) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: null W/b for layer %d", l);
+    int ndev = 0;
+    if (int st = pcd_get_device_count(&ndev)) return st;
+
+    std::unique_ptr<pcd_model> m(new pcd_model());
+    HIP_TRY(hipGetDevice(&m->device));
+    m->L = levels;
+    m->s.assign(sizes, sizes + levels);
+    m->P.resize(levels);
+    for (int l = 0; l < levels; ++l) m->P[l] = (int)round_up(sizes[l], kFeatPad);
+    m->act = activation;
+    m->ffg = ffg ? 1 : 0;
+    m->dtype = dtype;
+    m->eta = eta;
+    m->act_reg = act_reg;
+    m->prec.assign(precisions, precisions + levels);
+    m->W.assign(levels, nullptr);
+    m->WT.assign(levels, nullptr);
+    m->bias.assign(levels, nullptr);
+    const int ob = op_bytes(dtype);
+    std::vector<void*> owned;
+    auto cleanup = [&]() { for (void* p : owned) (void)hipFree(p); };
+    for (int l = 1; l < levels; ++l) {
+        const int lo = sizes[l - 1], sz = sizes[l];
+        const int Rlo = (int)round_up(lo, kRowPad), Rsz = (int)round_up(sz, kRowPad);
+        int st;
+        void *w = nullptr, *wt = nullptr, *bb = nullptr, *tmp = nullptr;
+        if ((st = dev_alloc_zero(owned, &w, (size_t)Rlo * m->P[l] * ob)) ||
+            (st = dev_alloc_zero(owned, &wt, (size_t)Rsz * m->P[l - 1] * ob)) ||
+            (st = dev_alloc_zero(owned, &bb, (size_t)m->P[l - 1] * 4)) ||
+            (st = dev_alloc_zero(owned, &tmp, (size_t)lo * sz * 4))) {
+            cleanup();
+            return st;
+        }
+        hipError_t e = hipMemcpy(tmp, W[l - 1], (size_t)lo * sz * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(bb, b[l - 1], (size_t)lo * 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) { cleanup(); return from_hip(e, "hipMemcpy(weights)"); }
+        // W_l as stored ([lo x sz] -> [Rlo x P_l]) and transposed ([sz x lo] -> [Rsz x P_{l-1}]).
+        int grid1 = (int)std::min<size_t>(((size_t)Rlo * m->P[l] + 255) / 256, 8192);
+        int grid2 = (int)std::min<size_t>(((size_t)Rsz * m->P[l - 1] + 255) / 256, 8192);
+        switch (dtype) {
+        case PCD_F32:
+            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l]);
+            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1]);
+            break;
+        case PCD_BF16:
+            hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l]);
+            hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1]);
+            break;
+        default:
+            hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l]);
+            hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1]);
+            break;
+        }
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) { cleanup(); return from_hip(e, "weight packing"); }
+        (void)hipFree(tmp);
+        owned.pop_back();
+        m->W[l] = w;
+        m->WT[l] = wt;
+        m->bias[l] = (float*)bb;
+    }
+    *out = m.release();
+    return PCD_SUCCESS;
+}
+
+int pcd_pc_model_destroy(pcd_model* m) {
+    if (!m) return PCD_SUCCESS;
+    (void)hipDeviceSynchronize();
+    for (auto& w : m->ws) free_workspace(*w);
+    for (int l = 1; l < m->L; ++l) {
+        (void)hipFree(m->W[l]);
+        (void)hipFree(m->WT[l]);
+        (void)hipFree(m->bias[l]);
+    }
+    delete m;
+    return PCD_SUCCESS;
+}
+
+int pcd_pc_model_info(const pcd_model* m, int* levels, int* sizes, int max_sizes, int* dtype) {
+    if (!m) return fail(PCD_NOT_INITIALIZED, "null model");
+    if (levels) *levels = m->L;
+    if (dtype) *dtype = m->dtype;
+    if (sizes)
+        for (int l = 0; l < m->L && l < max_sizes; ++l) sizes[l] = m->s[l];
+    return PCD_SUCCESS;
+}
+
+int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
+    if (int st = check_model(m)) return st;
+    if (!name) return fail(PCD_INVALID_VALUE, "null option name");
+    std::lock_guard<std::mutex> g(m->mu);
+    std::string n(name);
+    if (n == "use_graph") m->use_graph = value ? 1 : 0;
+    else if (n == "tile") {
+        if (value != 0 && value != 64 && value != 128 && value != 256)
+            return fail(PCD_INVALID_VALUE, "tile must be 0, 64, 128 or 256");
+        m->tile_m = m->tile_n = value;
+    } else if (n == "profile") m->profile = value ? 1 : 0;
+    else return fail(PCD_INVALID_VALUE, "unknown option '%s'", name);
+    // cached graphs were captured with the old options
+    for (auto& w : m->ws) {
+        for (auto& p : w->plans) {
+            if (p->exec) (void)hipGraphExecDestroy(p->exec);
+            if (p->graph) (void)hipGraphDestroy(p->graph);
+            if (p->energy_out) (void)hipFree(p->energy_out);
+        }
+        w->plans.clear();
+    }
+    return PCD_SUCCESS;
+}
+
+int pcd_pc_profile_result(pcd_model* m, float* err_ms, float* upd_ms, int* launches) {
+    if (int st = check_model(m)) return st;
+    if (err_ms) *err_ms = m->prof_err_ms;
+    if (upd_ms) *upd_ms = m->prof_upd_ms;
+    if (launches) *launches = m->prof_launches;
+    return PCD_SUCCESS;
+}
+
+static int copy_out_rows(float* dst, int cols, const float* src, int ld, int rows, hipStream_t s) {
+    HIP_TRY(hipMemcpy2DAsync(dst, (size_t)cols * 4, src, (size_t)ld * 4, (size_t)cols * 4, rows,
+                             hipMemcpyDeviceToDevice, s));
+    return PCD_SUCCESS;
+}
+
+int pcd_pc_relax(pcd_model* m, const float* x0, int batch, int steps, float* out_top, float* out_states,
+                 float* out_energy, void* stream_) {
+    if (int st = check_model(m)) return st;
+    if (batch < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
+    if (steps < 1) return fail(PCD_INVALID_VALUE, "inferenceSteps must be >= 1, got %d", steps);
+    if (!x0 || !out_top) return fail(PCD_INVALID_VALUE, "pcd_pc_relax: null pointer");
+    hipStream_t s = (hipStream_t)stream_;
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    Workspace* w = nullptr;
+    if (int st = ensure_workspace(m, s, batch, &w)) return st;
+    const int L = m->L;
+    const int tile = choose_tile(m, batch);
+    HIP_TRY(hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, batch,
+                             hipMemcpyDeviceToDevice, s));
+    float* energy_dst = nullptr;
+    if (m->profile) {
+        // Eager run with per-phase events; the energy buffer is the caller's.
+        PhaseTimer timer;
+        int st = enqueue_relax(m, w, batch, steps, tile, out_energy, nullptr, nullptr, nullptr, 0, 0, 0.f, nullptr,
+                               nullptr, s, &timer);
+        if (st) return st;
+        HIP_TRY(hipStreamSynchronize(s));
+        double te = 0, tu = 0;
+        for (size_t i = 0; i < timer.err.size(); ++i) {
+            float a = 0, b2 = 0;
+            HIP_TRY(hipEventElapsedTime(&a, timer.err[i].first, timer.err[i].second));
+            HIP_TRY(hipEventElapsedTime(&b2, timer.upd[i].first, timer.upd[i].second));
+            te += a;
+            tu += b2;
+        }
+        for (size_t i = 0; i < timer.err.size(); ++i) {
+            (void)hipEventDestroy(timer.err[i].first);
+            (void)hipEventDestroy(timer.err[i].second);
+            (void)hipEventDestroy(timer.upd[i].second);
+        }
+        m->prof_launches = (int)timer.err.size();
+        m->prof_err_ms = m->prof_launches ? (float)(te / m->prof_launches) : 0.f;
+        m->prof_upd_ms = m->prof_launches ? (float)(tu / m->prof_launches) : 0.f;
+    } else if (m->use_graph) {
+        int st = PCD_SUCCESS;
+        Plan* p = get_plan(m, w, batch, steps, out_energy != nullptr, tile, &st);
+        if (!p) return st;
+        HIP_TRY(hipGraphLaunch(p->exec, s));
+        energy_dst = p->energy_out;
+    } else {
+        int st = enqueue_relax(m, w, batch, steps, tile, out_energy, nullptr, nullptr, nullptr, 0, 0, 0.f, nullptr,
+                               nullptr, s, nullptr);
+        if (st) return st;
+    }
+    if (int st = copy_out_rows(out_top, m->s[L - 1], w->M[L - 1], m->P[L - 1], batch, s)) return st;
+    if (out_states) {
+        size_t off = 0;
+        for (int l = 0; l < L; ++l) {
+            if (int st = copy_out_rows(out_states + off, m->s[l], w->M[l], m->P[l], batch, s)) return st;
+            off += (size_t)batch * m->s[l];
+        }
+    }
+    if (out_energy && energy_dst)
+        HIP_TRY(hipMemcpyAsync(out_energy, energy_dst, (size_t)steps * batch * 4, hipMemcpyDeviceToDevice, s));
+    return PCD_SUCCESS;
+}
+
+int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_offsets, const int* steps, int requests,
+                        int exit_rule, float exit_threshold, int* steps_used, float* out_top, float* out_energy,
+                        void* stream_) {
+    if (int st = check_model(m)) return st;
+    if (requests < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
+    if (!x0_packed || !row_offsets || !steps || !steps_used || !out_top)
+        return fail(PCD_INVALID_VALUE, "pcd_pc_relax_ragged: null pointer");
+    if (exit_rule < PCD_EXIT_NONE || exit_rule > PCD_EXIT_ABSOLUTE)
+        return fail(PCD_INVALID_VALUE, "unknown exit rule %d", exit_rule);
+    if (row_offsets[0] != 0) return fail(PCD_INVALID_VALUE, "row_offsets[0] must be 0");
+    int tmax = 0;
+    for (int r = 0; r < requests; ++r) {
+        if (row_offsets[r + 1] <= row_offsets[r]) return fail(PCD_INVALID_VALUE, "request %d has no rows", r);
+        if (steps[r] < 1) return fail(PCD_INVALID_VALUE, "request %d: steps must be >= 1", r);
+        tmax = std::max(tmax, steps[r]);
+    }
+    const int rows = row_offsets[requests];
+    hipStream_t s = (hipStream_t)stream_;
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    Workspace* w = nullptr;
+    if (int st = ensure_workspace(m, s, rows, &w)) return st;
+    const int L = m->L;
+    const int tile = choose_tile(m, rows);
+    // Small per-call tables: rows' request ids, request offsets, exit state.
+    std::vector<int> row_req(rows);
+    for (int r = 0; r < requests; ++r)
+        for (int i = row_offsets[r]; i < row_offsets[r + 1]; ++i) row_req[i] = r;
+    const size_t tbytes = (size_t)rows * 4 + (size_t)(requests + 1) * 4 + (size_t)requests * 4 * 3;
+    void* tables = nullptr;
+    if (int st = pool_alloc(&tables, tbytes, s)) return st;
+    int* d_row_req = (int*)tables;
+    int* d_offsets = d_row_req + rows;
+    int* d_done = d_offsets + requests + 1;
+    float* d_prev = (float*)(d_done + requests);
+    float* d_last = d_prev + requests;
+    std::vector<char> host(tbytes, 0);
+    std::memcpy(host.data(), row_req.data(), (size_t)rows * 4);
+    std::memcpy(host.data() + (size_t)rows * 4, row_offsets, (size_t)(requests + 1) * 4);
+    std::memcpy(host.data() + (size_t)(rows + requests + 1) * 4, steps, (size_t)requests * 4);
+    int st = PCD_SUCCESS;
+    hipError_t e = hipMemcpyAsync(tables, host.data(), tbytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0_packed, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, rows,
+                             hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) st = from_hip(e, "ragged upload");
+    if (!st)
+        st = enqueue_relax(m, w, rows, tmax, tile, nullptr, d_row_req, d_done, d_offsets, requests, exit_rule,
+                           exit_threshold, d_prev, d_last, s, nullptr);
+    if (!st) st = copy_out_rows(out_top, m->s[L - 1], w->M[L - 1], m->P[L - 1], rows, s);
+    std::vector<float> last(requests);
+    if (!st) {
+        e = hipMemcpyAsync(steps_used, d_done, (size_t)requests * 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipMemcpyAsync(last.data(), d_last, (size_t)requests * 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) st = from_hip(e, "ragged download");
+    }
+    if (!st && out_energy) std::memcpy(out_energy, last.data(), (size_t)requests * 4);
+    pool_free(tables, s);
+    return st;
+}
+
+}  // extern "C"

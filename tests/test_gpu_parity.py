@@ -1,0 +1,199 @@
+"""GPU parity of the relaxation against the CPU oracle, through the C ABI.
+
+Tolerances use the reference tests' bound |a-b| <= tol*(1+|b|)
+(BatchedPcForwardTests.cs:67):
+  fp32                          1e-4 (the target the path is held to)
+  16-bit operands vs the oracle run with the same operand rounding   2e-3
+  bf16 operands vs the fp32 oracle                                     2e-2
+"""
+import numpy as np
+import pytest
+
+from tests.gpu_util import build_case, run_gpu, run_oracle
+from tests.netgen import close, max_rel
+
+pytestmark = pytest.mark.gpu
+
+ACTS = ["linear", "tanh", "relu", "sigmoid", "gelu"]
+
+
+def _report(name, **errs):
+    print(name, " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+
+
+def test_c1_reference_config_fp32(oracle):
+    # 784-256-256-10 tanh fp32, B=64, T=20, eta=0.1, x0~U[0,1], Xavier, b=0
+    snap, W, b, P, x = build_case([784, 256, 256, 10], "tanh", 0.1, batch=64, xdist="uniform01", seed=0)
+    top, st, en = run_gpu(snap, x, 20, states=True, energy=True)
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 20, states=True, energy=True)
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren),
+                states=max(max_rel(a, r) for a, r in zip(st, rst)))
+    _report("c1", **errs)
+    assert all(v < 1e-4 for v in errs.values()), errs
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("variant", ["plain", "ffg", "actreg_prec"])
+def test_activations_and_options_fp32(oracle, act, variant):
+    kw = dict(ffg=variant == "ffg", act_reg=0.01 if variant == "actreg_prec" else 0.0,
+              precisions=[1.0, 0.7, 1.3, 1.0] if variant == "actreg_prec" else None)
+    # odd sizes exercise every padding path
+    snap, W, b, P, x = build_case([37, 70, 19, 5], act, 0.1, batch=13, bias_scale=0.2, seed=3, **kw)
+    top, st, en = run_gpu(snap, x, 12, states=True, energy=True)
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 12, states=True, energy=True)
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren),
+                states=max(max_rel(a, r) for a, r in zip(st, rst)))
+    _report(f"{act}/{variant}", **errs)
+    assert all(v < 1e-4 for v in errs.values()), errs
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("act", ["tanh", "gelu"])
+def test_16bit_operands(oracle, dtype, act):
+    snap, W, b, P, x = build_case([96, 130, 64, 16], act, 0.05, batch=40, init="fanin", seed=5)
+    top, _, en = run_gpu(snap, x, 15, dtype=dtype, energy=True)
+    rtop, _, ren = run_oracle(oracle, snap, W, b, P, x, 15, dtype=dtype, energy=True)
+    ftop, _, fen = run_oracle(oracle, snap, W, b, P, x, 15, dtype="f32", energy=True)
+    errs = dict(top_same_rounding=max_rel(top, rtop), energy_same_rounding=max_rel(en, ren),
+                top_vs_f32=max_rel(top, ftop), energy_vs_f32=max_rel(en, fen))
+    _report(f"{dtype}/{act}", **errs)
+    assert errs["top_same_rounding"] < 2e-3 and errs["energy_same_rounding"] < 2e-3, errs
+    assert errs["top_vs_f32"] < 2e-2 and errs["energy_vs_f32"] < 2e-2, errs
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("tile", [64, 128, 256])
+def test_every_tile_shape(oracle, dtype, tile):
+    snap, W, b, P, x = build_case([300, 260, 200], "tanh", 0.1, batch=300, seed=7, bias_scale=0.1)
+    top, _, en = run_gpu(snap, x, 6, dtype=dtype, energy=True, options={"tile": tile})
+    rtop, _, ren = run_oracle(oracle, snap, W, b, P, x, 6, dtype=dtype, energy=True)
+    tol = 1e-4 if dtype == "f32" else 2e-3
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren))
+    _report(f"tile{tile}/{dtype}", **errs)
+    assert all(v < tol for v in errs.values()), errs
+
+
+def test_graph_and_eager_agree_bit_for_bit():
+    snap, W, b, P, x = build_case([64, 128, 32], "tanh", 0.1, batch=50, seed=9)
+    g_top, _, g_en = run_gpu(snap, x, 7, energy=True, options={"use_graph": 1})
+    e_top, _, e_en = run_gpu(snap, x, 7, energy=True, options={"use_graph": 0})
+    assert np.array_equal(g_top, e_top) and np.array_equal(g_en, e_en)
+
+
+def test_repeated_calls_and_changing_batches(oracle):
+    from predicitivecoding_amd import PcDeviceModel
+    snap, W, b, P, x = build_case([48, 96, 24], "tanh", 0.1, batch=70, seed=11)
+    m = PcDeviceModel(snap, "f32")
+    try:
+        for B, T in [(70, 5), (3, 5), (70, 5), (33, 9), (1, 2), (70, 5)]:
+            top, _, en = m.relax(x[:B], T, want_energy=True)
+            rtop, _, ren = run_oracle(oracle, snap, W, b, P, x[:B], T, energy=True)
+            assert max_rel(top, rtop) < 1e-4 and max_rel(en, ren) < 1e-4, (B, T)
+    finally:
+        m.close()
+
+
+def test_rows_are_independent_bit_for_bit():
+    snap, W, b, P, x = build_case([80, 64, 40], "tanh", 0.1, batch=200, seed=13)
+    perm = np.random.default_rng(0).permutation(200)
+    top, _, en = run_gpu(snap, x, 5, energy=True)
+    ptop, _, pen = run_gpu(snap, x[perm], 5, energy=True)
+    assert np.array_equal(top[perm], ptop) and np.array_equal(en[:, perm], pen)
+    one, _, _ = run_gpu(snap, x[17:18], 5)
+    assert np.array_equal(one[0], top[17])
+
+
+def test_two_level_network():
+    # L = 2: a single weight matrix, top is the only free layer
+    from tests.netgen import make_inputs
+    import oracle.pc_oracle as O
+    snap, W, b, P, x = build_case([33, 7], "sigmoid", 0.2, batch=5, seed=15, bias_scale=0.3)
+    top, _, en = run_gpu(snap, x, 30, energy=True)
+    rtop, _, ren = run_oracle(O, snap, W, b, P, x, 30, energy=True)
+    assert max_rel(top, rtop) < 1e-4 and max_rel(en, ren) < 1e-4
+
+
+def test_c2_shape_row_subset(oracle):
+    # 1024-1024-1024-1024-256 tanh fp32, B=1024, T=50, eta=0.05, x0~N(0,1).
+    # Rows are independent, so the oracle settles a subset of rows exactly.
+    snap, W, b, P, x = build_case([1024, 1024, 1024, 1024, 256], "tanh", 0.05, batch=1024, seed=2)
+    top, _, en = run_gpu(snap, x, 50, energy=True)
+    rows = np.array([0, 1, 511, 1023])
+    rtop, _, ren = run_oracle(oracle, snap, W, b, P, x[rows], 50, energy=True)
+    errs = dict(top=max_rel(top[rows], rtop), energy=max_rel(en[:, rows], ren))
+    _report("c2-subset", **errs)
+    assert all(v < 1e-4 for v in errs.values()), errs
+
+
+def test_ragged_requests_with_exit(oracle):
+    from predicitivecoding_amd import PcDeviceModel
+    sizes = [40, 64, 32, 8]
+    snap, W, b, P, _ = build_case(sizes, "tanh", 0.1, seed=17)
+    rng = np.random.default_rng(3)
+    counts = [1, 5, 17, 2, 64, 9, 3, 30]
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    x = (rng.standard_normal((offs[-1], sizes[0])) * 0.3).astype(np.float32)
+    steps = rng.integers(3, 40, len(counts)).astype(np.int32)
+    m = PcDeviceModel(snap, "f32")
+    try:
+        # no exit: every request runs its own budget
+        used, fe, top = m.relax_ragged(x, offs, steps, "none")
+        rused, rfe, rtop = oracle.ragged_relax(sizes, "tanh", 0.1, W, b, P, x, offs, steps, "none")
+        assert np.array_equal(used, steps) and np.array_equal(rused, steps)
+        assert max_rel(top, rtop) < 1e-4 and max_rel(fe, rfe) < 1e-4
+        # absolute exit (energy per sample below a threshold) and the reference's relative rule
+        for rule, thr in [("absolute", 1.0), ("absolute", 0.8), ("relative", 1e-2), ("relative", 3e-2)]:
+            used, fe, top = m.relax_ragged(x, offs, steps, rule, thr)
+            rused, rfe, rtop = oracle.ragged_relax(sizes, "tanh", 0.1, W, b, P, x, offs, steps, rule, thr)
+            _report(f"ragged/{rule}", used_diff=float(np.max(np.abs(used - rused))))
+            assert np.array_equal(used, rused), (rule, used, rused)
+            assert max_rel(top, rtop) < 1e-4 and max_rel(fe, rfe) < 1e-4
+            assert np.any(used < steps), "the exit rule never fired"
+    finally:
+        m.close()
+
+
+def test_gemm_entry_points():
+    from predicitivecoding_amd import DeviceTensor, TensorOps
+    from predicitivecoding_amd.gemm import HipGemmProvider
+    # LlmDeviceTests.cs:41-55 known answer
+    a = DeviceTensor.from_host(np.array([[1, 2, 3], [4, 5, 6]], np.float32))
+    bb = DeviceTensor.from_host(np.array([[7, 8], [9, 10], [11, 12]], np.float32))
+    c = TensorOps.mat_mul(a, bb).to_host()
+    assert c.tolist() == [[58, 64], [139, 154]]
+    rng = np.random.default_rng(0)
+    for (m, k, n) in [(1, 1, 1), (37, 53, 29), (200, 130, 333), (64, 64, 64)]:
+        for ta in (0, 1):
+            for tb in (0, 1):
+                A = rng.standard_normal((k, m) if ta else (m, k)).astype(np.float32)
+                B = rng.standard_normal((n, k) if tb else (k, n)).astype(np.float32)
+                C0 = rng.standard_normal((m, n)).astype(np.float32)
+                want = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64) + 0.5 * C0
+                dc = DeviceTensor.from_host(C0)
+                TensorOps.mat_mul(DeviceTensor.from_host(A), DeviceTensor.from_host(B), bool(ta), bool(tb),
+                                  0.5, out=dc)
+                got = dc.to_host()
+                assert np.max(np.abs(got - want)) < 1e-3 * (1 + np.max(np.abs(want))), (m, k, n, ta, tb)
+    # MixedGemmTests.cs:43-52: mixed provider within 1e-2*(1+|x|) of float
+    p = HipGemmProvider()
+    A = rng.random((8, 16)).astype(np.float32)
+    B = rng.random((16, 4)).astype(np.float32)
+    assert close(p.mat_mul_mixed(A, 8, 16, B, 4), A.astype(np.float64) @ B, 1e-2)
+    assert close(p.mat_mul(A, 8, 16, B, 4), A.astype(np.float64) @ B, 1e-5)
+
+
+def test_device_errors_are_status_codes():
+    from predicitivecoding_amd import DeviceException, DeviceStatus, PcDeviceModel
+    import ctypes
+    from predicitivecoding_amd import _native
+    snap, W, b, P, x = build_case([16, 8], "tanh", 0.1, batch=2)
+    m = PcDeviceModel(snap, "f32")
+    try:
+        L = _native.lib()
+        assert L.pcd_pc_relax(m.handle, None, 2, 3, None, None, None, None) == DeviceStatus.InvalidValue
+        assert L.pcd_pc_relax(m.handle, 1, 0, 3, 1, None, None, None) == DeviceStatus.InvalidValue
+        assert L.pcd_pc_relax(m.handle, 1, 2, 0, 1, None, None, None) == DeviceStatus.InvalidValue
+        with pytest.raises(DeviceException):
+            m.set_option("tile", 96)
+    finally:
+        m.close()
