@@ -114,7 +114,8 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--tile", type=int, default=0)
+    ap.add_argument("--tile", type=int, default=0, help="force the GEMM tile rows (and columns unless --tile-n)")
+    ap.add_argument("--tile-n", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build runs the relaxation on a single MI355X "
@@ -132,6 +133,8 @@ def main():
     model = PcDeviceModel(snap, cfg["dtype"])
     if args.tile:
         model.set_option("tile", args.tile)
+        if args.tile_n:
+            model.set_option("tile_n", args.tile_n)
     x = make_inputs(cfg)
     top = torch.empty((B, sizes[-1]), device="cuda", dtype=torch.float32)
     torch.cuda.synchronize()

@@ -120,29 +120,53 @@ struct PhaseArgs {
 
 // ------------------------------------------------------------ scalar helpers
 
-__device__ __forceinline__ float act_f(int act, float x) {
+// tanh(x) = sign(x) (1 - 2 / (exp(2|x|) + 1)), from the definition, with the
+// hardware exp2 and reciprocal.  Absolute error ~1e-7 (relative error grows
+// only where |tanh| is below ~1e-3, where the absolute error is what the
+// relaxation sees); saturates to +-1 for large |x|.
+__device__ __forceinline__ float fast_tanh(float x) {
+    const float e = __builtin_amdgcn_exp2f(fabsf(x) * 2.8853900817779268f);  // exp(2|x|)
+    const float t = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
+    return copysignf(t, x);
+}
+
+// f(pre) and f'(pre) together (Activation.cs:34-132; GELU-tanh and its
+// derivative from pre, Layers.cs:42-50 and Autograd.cs:313-318), sharing the
+// one transcendental evaluation both need.
+__device__ __forceinline__ void act_eval(int act, float x, float& y, float& dy) {
     switch (act) {
-    case ACT_TANH: return tanhf(x);
-    case ACT_RELU: return x > 0.f ? x : 0.f;
-    case ACT_SIGMOID: return 1.f / (1.f + expf(-x));
-    case ACT_GELU: return 0.5f * x * (1.f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
-    default: return x;
+    case ACT_TANH: {
+        y = fast_tanh(x);
+        dy = 1.f - y * y;
+        break;
+    }
+    case ACT_RELU:
+        y = x > 0.f ? x : 0.f;
+        dy = x > 0.f ? 1.f : 0.f;
+        break;
+    case ACT_SIGMOID: {
+        y = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+        dy = y * (1.f - y);
+        break;
+    }
+    case ACT_GELU: {
+        const float c = 0.7978845608f, a = 0.044715f;
+        const float x2 = x * x;
+        const float t = fast_tanh(c * (x + a * x2 * x));
+        y = 0.5f * x * (1.f + t);
+        dy = 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * (c * (1.f + 3.f * a * x2));
+        break;
+    }
+    default:
+        y = x;
+        dy = 1.f;
     }
 }
 
-// f'(pre) given y = f(pre): Activation.cs:86-132; GELU from pre (Autograd.cs:313-318).
-__device__ __forceinline__ float act_df(int act, float pre, float y) {
-    switch (act) {
-    case ACT_TANH: return 1.f - y * y;
-    case ACT_RELU: return pre > 0.f ? 1.f : 0.f;
-    case ACT_SIGMOID: return y * (1.f - y);
-    case ACT_GELU: {
-        const float c = 0.7978845608f, a = 0.044715f;
-        float t = tanhf(c * (pre + a * pre * pre * pre));
-        return 0.5f * (1.f + t) + 0.5f * pre * (1.f - t * t) * (c * (1.f + 3.f * a * pre * pre));
-    }
-    default: return 1.f;
-    }
+__device__ __forceinline__ float act_f(int act, float x) {
+    float y, dy;
+    act_eval(act, x, y, dy);
+    return y;
 }
 
 // Round-to-nearest-even fp32 -> bf16 with NaN kept NaN (TensorUtils.cs:386-395).
@@ -200,28 +224,58 @@ __device__ __forceinline__ bool row_active(const PhaseArgs& a, int row) {
     return a.row_req == nullptr || a.t < a.done_at[a.row_req[row]];
 }
 
-// 16-byte unit u of LDS row r lives at unit u ^ (r & 7).
-__device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 7); }
-
-constexpr int kStageBytes = 128;      // K bytes per row per LDS stage
-constexpr int kUnits = kStageBytes / 16;
+// LDS layout of one pipeline stage: rows of kRowBytes (the K slice of one
+// A or B row), A rows first, then B rows.  The four 16-byte units of row R sit
+// at unit u ^ ((R >> 2) & 3).  Measured on gfx950 with SQ_LDS_BANK_CONFLICT,
+// this makes the fragment reads (32 consecutive rows x 2 units per wave, one
+// ds_read_b128 each) conflict-free; XOR keys built from other row bits leave
+// a 2-way conflict.
+constexpr int kRowBytes = 64;                 // K bytes per row per stage
+constexpr int kUnits = kRowBytes / 16;        // 16-byte units per row
+__device__ __forceinline__ int swz(int row, int unit) { return unit ^ ((row >> 2) & 3); }
 
 template <int BM, int BN> struct TileCfg {
     static constexpr int WM = 2, WN = 2;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
-    static constexpr int LA = BM * kUnits / 256, LB = BN * kUnits / 256;
-    static constexpr int stage_bytes = (BM + BN) * kStageBytes;
-    static_assert(FM >= 1 && FN >= 1 && LA >= 1 && LB >= 1, "tile too small");
+    static constexpr int stage_bytes = (BM + BN) * kRowBytes;
+    // Stages in the LDS ring: 4 (prefetch distance 3) unless that would keep
+    // a second workgroup off the CU; 256 x 128 runs 3 stages (72 KB) so two
+    // workgroups share a CU and one's epilogue overlaps the other's MFMAs.
+    static constexpr int NS = (BM == 256 && BN == 128) ? 3 : 4;
+    static constexpr int D = NS - 1;                      // prefetch distance (stages)
+    // Workgroups per CU the register budget is sized for (256 x 256 needs the
+    // whole register file of a SIMD for its 256 accumulators per lane).
+    static constexpr int OCC = (BM == 256 && BN == 256) ? 1 : 2;
+    static constexpr int ROWS_PER_LOAD = 64 * 16 / kRowBytes;             // rows one wave-wide load fills
+    static constexpr int QPW = (BM + BN) / ROWS_PER_LOAD / 4;             // loads per wave per stage
+    static_assert(FM >= 1 && FN >= 1 && QPW >= 1, "tile too small");
+    static_assert((BM + BN) % (4 * ROWS_PER_LOAD) == 0, "stage rows must split evenly over 4 waves");
 };
 
+// Direct global -> LDS copy of 16 bytes per lane (gfx950 global_load_lds_dwordx4):
+// lane l's bytes land at LDS address m0 + 16 l.  Issued as inline asm so the
+// compiler does not serialise it with a vmcnt(0) before every LDS read; the
+// kernel places its own vmcnt waits.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 template <typename OP, int BM, int BN, int EPI>
-__global__ void __launch_bounds__(256, 1)
+__global__ void __launch_bounds__(256, (TileCfg<BM, BN>::OCC))
 phase_kernel(const ProblemSet set, const PhaseArgs args) {
     using C = TileCfg<BM, BN>;
     constexpr int OPB = OpTraits<OP>::bytes;
-    constexpr int KE = kStageBytes / OPB;  // K elements per stage
-    __shared__ __attribute__((aligned(16))) char smem[2 * C::stage_bytes];
+    __shared__ __attribute__((aligned(16))) char smem[C::NS * C::stage_bytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -270,77 +324,89 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x16{};
 
-    typedef const __attribute__((address_space(1))) char GChar;
-    typedef const __attribute__((address_space(1))) u32x4 GVec;
-    GChar* Ag = (GChar*)P.A + (size_t)row0 * P.lda * OPB;
-    GChar* Bg = (GChar*)P.B + (size_t)col0 * P.ldb * OPB;
+    const char* Ag = (const char*)P.A + (size_t)row0 * P.lda * OPB;
+    const char* Bg = (const char*)P.B + (size_t)col0 * P.ldb * OPB;
     const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
+    constexpr int KE = kRowBytes / OPB;  // K elements per stage
     const int nk = P.K / KE;
 
-    u32x4 ra[C::LA], rb[C::LB];
-    auto gload = [&](int kt) PCD_INLINE {
-        const size_t kb = (size_t)kt * kStageBytes;
+    // This lane's source of each of its wave's QPW loads per stage: combined
+    // stage row R = q*ROWS_PER_LOAD + lane/4 (A rows, then B rows), physical
+    // unit lane%4, which holds logical unit swz(R, lane%4).
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const char* src[C::QPW];
 #pragma unroll
-        for (int i = 0; i < C::LA; ++i) {
-            int u = tid + i * 256, r = u / kUnits, j = u % kUnits;
-            ra[i] = *(GVec*)(Ag + r * lda_b + kb + j * 16);
+    for (int i = 0; i < C::QPW; ++i) {
+        const int q = wave_u * C::QPW + i;
+        const int R = q * C::ROWS_PER_LOAD + (lane >> 2);
+        const int unit = swz(R, lane & 3);
+        src[i] = R < BM ? Ag + (size_t)R * lda_b + unit * 16 : Bg + (size_t)(R - BM) * ldb_b + unit * 16;
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+    auto issue_stage = [&](int kt) PCD_INLINE {
+        const uint32_t base = lds0 + (kt % C::NS) * C::stage_bytes + wave_u * C::QPW * 1024;
+#pragma unroll
+        for (int i = 0; i < C::QPW; ++i) lds_dma16(src[i] + (size_t)kt * kRowBytes, base + i * 1024);
+    };
+    // Fragments of K chunk c (32 bytes per row) of the stage in `slot`.
+    const int half = lane >> 5, lr = lane & 31;
+    auto read_frags = [&](int slot, int c, u32x4* a, u32x4* b) PCD_INLINE {
+        const char* st = smem + slot * C::stage_bytes;
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i) {
+            const int R = wm * C::WTM + i * 32 + lr;
+            a[i] = *(const u32x4*)(st + R * kRowBytes + swz(R, 2 * c + half) * 16);
         }
 #pragma unroll
-        for (int i = 0; i < C::LB; ++i) {
-            int u = tid + i * 256, r = u / kUnits, j = u % kUnits;
-            rb[i] = *(GVec*)(Bg + r * ldb_b + kb + j * 16);
+        for (int j = 0; j < C::FN; ++j) {
+            const int R = BM + wn * C::WTN + j * 32 + lr;
+            b[j] = *(const u32x4*)(st + R * kRowBytes + swz(R, 2 * c + half) * 16);
         }
     };
-    auto sstore = [&](int stage) PCD_INLINE {
-        char* sA = smem + stage * C::stage_bytes;
-        char* sB = sA + BM * kStageBytes;
-#pragma unroll
-        for (int i = 0; i < C::LA; ++i) {
-            int u = tid + i * 256, r = u / kUnits, j = u % kUnits;
-            *(u32x4*)(sA + r * kStageBytes + swz(r, j) * 16) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < C::LB; ++i) {
-            int u = tid + i * 256, r = u / kUnits, j = u % kUnits;
-            *(u32x4*)(sB + r * kStageBytes + swz(r, j) * 16) = rb[i];
-        }
+    auto mfmas = [&](const u32x4* a, const u32x4* b) PCD_INLINE {
+        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+            static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                mfma_chunk<OP>(acc[decltype(I)::value][decltype(J)::value], a[decltype(I)::value], b[decltype(J)::value]);
+            });
+        });
     };
-    auto compute = [&](int stage) PCD_INLINE {
-        const char* sA = smem + stage * C::stage_bytes;
-        const char* sB = sA + BM * kStageBytes;
-        const int half = lane >> 5, lr = lane & 31;
-#pragma unroll
-        for (int c = 0; c < kStageBytes / 32; ++c) {
-            u32x4 a[C::FM], b[C::FN];
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i) {
-                int r = wm * C::WTM + i * 32 + lr;
-                a[i] = *(const u32x4*)(sA + r * kStageBytes + swz(r, 2 * c + half) * 16);
-            }
-#pragma unroll
-            for (int j = 0; j < C::FN; ++j) {
-                int r = wn * C::WTN + j * 32 + lr;
-                b[j] = *(const u32x4*)(sB + r * kStageBytes + swz(r, 2 * c + half) * 16);
-            }
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-                for (int j = 0; j < C::FN; ++j) mfma_chunk<OP>(acc[i][j], a[i], b[j]);
+    // Wait until stage `next` has landed for this wave, given how many later
+    // stages are still in flight, then make it visible to all waves.
+    auto stage_ready = [&](int next) PCD_INLINE {
+        const int later = min(C::D - 1, nk - 1 - next);
+        if constexpr (C::D >= 3) {
+            if (later >= 2) wait_vmcnt<2 * C::QPW>();
+            else if (later == 1) wait_vmcnt<C::QPW>();
+            else wait_vmcnt<0>();
+        } else {
+            if (later >= 1) wait_vmcnt<C::QPW>();
+            else wait_vmcnt<0>();
         }
+        __syncthreads();
     };
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        if (kt + 1 < nk) gload(kt + 1);
-        compute(kt & 1);
-        if (kt + 1 < nk) sstore((kt + 1) & 1);
-        __syncthreads();
+    u32x4 fa0[C::FM], fb0[C::FN], fa1[C::FM], fb1[C::FN];
+    static_assert(C::D == 2 || C::D == 3, "stage_ready handles prefetch distances 2 and 3");
+    for (int s2 = 0; s2 < C::D && s2 < nk; ++s2) issue_stage(s2);
+    stage_ready(0);
+    read_frags(0, 0, fa0, fb0);
+    // Steady state: the next stage's first fragments are read right after the
+    // barrier and consumed one MFMA group later.  The last stage is peeled off
+    // so no path through the loop skips those reads (a merge there makes the
+    // compiler wait for them before the second group).
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+        if (kt + C::D < nk) issue_stage(kt + C::D);
+        read_frags(kt % C::NS, 1, fa1, fb1);
+        mfmas(fa0, fb0);
+        stage_ready(kt + 1);
+        read_frags((kt + 1) % C::NS, 0, fa0, fb0);
+        mfmas(fa1, fb1);
     }
+    read_frags((nk - 1) % C::NS, 1, fa1, fb1);
+    mfmas(fa0, fb0);
+    mfmas(fa1, fb1);
 
     // ---- epilogue
-    const int half = lane >> 5, lr = lane & 31;
     // Row of register r of a block in row-block i: 8*(r/4) + 4*half + r%4.
     auto row_of = [&](int i, int r) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
     auto col_of = [&](int j) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + lr; };
@@ -363,9 +429,10 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                     if (cok && row < P.M && row_active(args, row)) {
                         const size_t idx = (size_t)row * P.ldo + col;
                         const float pre = acc[i][j][r] + bj;
-                        const float y = act_f(args.act, pre);
+                        float y, dy;
+                        act_eval(args.act, pre, y, dy);
                         const float e = P_low * (P.mlow[idx] - y);
-                        const float d = act_df(args.act, pre, y) * e;
+                        const float d = dy * e;
                         OpTraits<OP>::store(P.dout, idx, d);
                         if (P.eout) P.eout[idx] = e;
                         esum[r] += e * e * inv2p;

@@ -156,17 +156,25 @@ int launch_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid,
     return from_hip(hipGetLastError(), "phase_kernel launch");
 }
 
-template <typename OP>
-int launch_op(int tile, int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
-    switch (tile) {
-    case 64: return launch_tile<OP, 64, 64>(epi, set, args, grid, s);
-    case 128: return launch_tile<OP, 128, 128>(epi, set, args, grid, s);
-    case 256: return launch_tile<OP, 256, 256>(epi, set, args, grid, s);
-    default: return fail(PCD_INVALID_VALUE, "unsupported tile %d", tile);
-    }
+// GEMM tile shapes compiled into the library (rows x columns of the output).
+struct Tile {
+    int m, n;
+};
+bool tile_supported(Tile t) {
+    return (t.m == 64 && t.n == 64) || (t.m == 128 && t.n == 128) || (t.m == 256 && t.n == 128) ||
+           (t.m == 256 && t.n == 256);
 }
 
-int launch_phase(int dtype, int tile, int epi, const ProblemSet& set, const PhaseArgs& args, hipStream_t s) {
+template <typename OP>
+int launch_op(Tile tile, int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
+    if (tile.m == 64 && tile.n == 64) return launch_tile<OP, 64, 64>(epi, set, args, grid, s);
+    if (tile.m == 128 && tile.n == 128) return launch_tile<OP, 128, 128>(epi, set, args, grid, s);
+    if (tile.m == 256 && tile.n == 128) return launch_tile<OP, 256, 128>(epi, set, args, grid, s);
+    if (tile.m == 256 && tile.n == 256) return launch_tile<OP, 256, 256>(epi, set, args, grid, s);
+    return fail(PCD_INVALID_VALUE, "unsupported tile %d x %d", tile.m, tile.n);
+}
+
+int launch_phase(int dtype, Tile tile, int epi, const ProblemSet& set, const PhaseArgs& args, hipStream_t s) {
     int grid = 0;
     for (int i = 0; i < set.n; ++i) grid += set.p[i].tiles_m * set.p[i].tiles_n;
     if (grid == 0) return PCD_SUCCESS;
@@ -211,7 +219,8 @@ struct Workspace {
 };
 
 struct Plan {
-    int batch = 0, steps = 0, want_energy = 0, tile = 0, ffg = 0;
+    int batch = 0, steps = 0, want_energy = 0, ffg = 0;
+    Tile tile{0, 0};
     float* energy_out = nullptr;       // [steps x batch]
     hipGraphExec_t exec = nullptr;
     hipGraph_t graph = nullptr;
@@ -262,20 +271,20 @@ int dev_alloc_zero(std::vector<void*>& owned, void** out, size_t bytes) {
     return PCD_SUCCESS;
 }
 
-int choose_tile(const pcd_model* m, int batch) {
-    if (m->tile_m > 0) return m->tile_m;
-    if (batch <= 64) return 64;
+Tile choose_tile(const pcd_model* m, int batch) {
+    if (m->tile_m > 0) return Tile{m->tile_m, m->tile_n};
+    if (batch <= 64) return Tile{64, 64};
     if (m->dtype != PCD_F32 && batch >= 1024) {
         bool wide = true;
         for (int l = 0; l < m->L; ++l) wide = wide && m->s[l] >= 1024;
-        if (wide) return 256;
+        if (wide) return Tile{256, 128};
     }
-    return 128;
+    return Tile{128, 128};
 }
 
-int energy_slots(const pcd_model* m, int tile) {
+int energy_slots(const pcd_model* m, int tile_n) {
     int slots = 0;
-    for (int l = 1; l < m->L; ++l) slots += (int)((m->s[l - 1] + tile - 1) / tile) * 2;
+    for (int l = 1; l < m->L; ++l) slots += (int)((m->s[l - 1] + tile_n - 1) / tile_n) * 2;
     return slots;
 }
 
@@ -289,7 +298,7 @@ int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out
         w->stream = stream;
     }
     int need = (int)round_up((size_t)std::max(rows, 1), kRowPad);
-    int slots = energy_slots(m, 64);  // the smallest tile has the most slots
+    int slots = energy_slots(m, 64);  // the narrowest tile has the most slots
     if (w->cap >= need && w->slots_cap >= slots) {
         *out = w;
         return PCD_SUCCESS;
@@ -327,12 +336,12 @@ const void* state_operand(const pcd_model* m, const Workspace* w, int l) {
 
 // Problem sets of the two phases for a batch; problems beyond kMaxProblems
 // spill into further sets (still one phase: the problems are independent).
-void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, int tile, int ragged,
+void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile tile, int ragged,
                       std::vector<ProblemSet>& err, std::vector<ProblemSet>& upd, int* nslots) {
     err.clear();
     upd.clear();
     const int L = m->L;
-    const int tm = (batch + tile - 1) / tile;
+    const int tm = (batch + tile.m - 1) / tile.m;
     int slot = 0;
     for (int l = L - 1; l >= 1; --l) {   // error phase: widest K first is irrelevant; keep layer order
         if (err.empty() || err.back().n == kMaxProblems) { err.emplace_back(); err.back().n = 0; }
@@ -348,7 +357,7 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, int til
         p.N = m->s[l - 1];
         p.K = m->P[l];
         p.tiles_m = tm;
-        p.tiles_n = (p.N + tile - 1) / tile;
+        p.tiles_n = (p.N + tile.n - 1) / tile.n;
         p.tile_start = start;
         p.ldo = m->P[l - 1];
         p.bias = m->bias[l];
@@ -373,7 +382,7 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, int til
         p.N = m->s[l];
         p.K = m->P[l - 1];
         p.tiles_m = tm;
-        p.tiles_n = (p.N + tile - 1) / tile;
+        p.tiles_n = (p.N + tile.n - 1) / tile.n;
         p.tile_start = start;
         p.ldo = m->P[l];
         p.m = w->M[l];
@@ -404,7 +413,7 @@ struct PhaseTimer {
     std::vector<std::pair<hipEvent_t, hipEvent_t>> err, upd;
 };
 
-int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, int tile, float* energy_out,
+int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, Tile tile, float* energy_out,
                   const int* row_req, int* done_at, const int* row_offsets_dev, int requests, int exit_rule,
                   float exit_thr, float* prev_energy, float* last_energy, hipStream_t s, PhaseTimer* timer) {
     const int L = m->L;
@@ -435,8 +444,8 @@ int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, int tile, fl
             p.M = batch;
             p.N = m->s[l - 1];
             p.K = m->P[l];
-            p.tiles_m = (batch + tile - 1) / tile;
-            p.tiles_n = (p.N + tile - 1) / tile;
+            p.tiles_m = (batch + tile.m - 1) / tile.m;
+            p.tiles_n = (p.N + tile.n - 1) / tile.n;
             p.ldo = m->P[l - 1];
             p.bias = m->bias[l];
             p.m = w->M[l - 1];
@@ -482,10 +491,11 @@ int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, int tile, fl
     return PCD_SUCCESS;
 }
 
-Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy, int tile, int* status) {
+Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy, Tile tile, int* status) {
     *status = PCD_SUCCESS;
     for (auto& p : w->plans)
-        if (p->batch == batch && p->steps == steps && p->want_energy == want_energy && p->tile == tile) {
+        if (p->batch == batch && p->steps == steps && p->want_energy == want_energy && p->tile.m == tile.m &&
+            p->tile.n == tile.n) {
             p->last_use = ++m->clock;
             return p.get();
         }
@@ -733,8 +743,8 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     if (!dA || !dB || !dC) return fail(PCD_INVALID_VALUE, "pcd_gemm: null pointer");
     if (m < 1 || k < 1 || n < 1) return fail(PCD_INVALID_VALUE, "pcd_gemm: bad shape %d x %d x %d", m, k, n);
     hipStream_t s = (hipStream_t)stream_;
-    const int tile = (m <= 64 || n <= 64) ? 64 : 128;
-    const int mp = (int)round_up(m, tile), np = (int)round_up(n, tile), kp = (int)round_up(k, kFeatPad);
+    const Tile tile = (m <= 64 || n <= 64) ? Tile{64, 64} : Tile{128, 128};
+    const int mp = (int)round_up(m, tile.m), np = (int)round_up(n, tile.n), kp = (int)round_up(k, kFeatPad);
     const int ob = op_bytes(dtype);
     void *pa = nullptr, *pb = nullptr;
     int st;
@@ -769,8 +779,8 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     p.M = m;
     p.N = n;
     p.K = kp;
-    p.tiles_m = mp / tile;
-    p.tiles_n = np / tile;
+    p.tiles_m = mp / tile.m;
+    p.tiles_n = np / tile.n;
     p.ldo = n;
     p.m = dC;
     PhaseArgs a;
@@ -916,9 +926,13 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
     std::string n(name);
     if (n == "use_graph") m->use_graph = value ? 1 : 0;
     else if (n == "tile") {
-        if (value != 0 && value != 64 && value != 128 && value != 256)
+        if (value != 0 && !tile_supported(Tile{value, value}))
             return fail(PCD_INVALID_VALUE, "tile must be 0, 64, 128 or 256");
         m->tile_m = m->tile_n = value;
+    } else if (n == "tile_n") {
+        if (m->tile_m == 0 || !tile_supported(Tile{m->tile_m, value}))
+            return fail(PCD_INVALID_VALUE, "tile_n: unsupported tile %d x %d (set tile first)", m->tile_m, value);
+        m->tile_n = value;
     } else if (n == "profile") m->profile = value ? 1 : 0;
     else return fail(PCD_INVALID_VALUE, "unknown option '%s'", name);
     // cached graphs were captured with the old options
@@ -959,7 +973,7 @@ int pcd_pc_relax(pcd_model* m, const float* x0, int batch, int steps, float* out
     Workspace* w = nullptr;
     if (int st = ensure_workspace(m, s, batch, &w)) return st;
     const int L = m->L;
-    const int tile = choose_tile(m, batch);
+    const Tile tile = choose_tile(m, batch);
     HIP_TRY(hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, batch,
                              hipMemcpyDeviceToDevice, s));
     float* energy_dst = nullptr;
@@ -1033,7 +1047,7 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
     Workspace* w = nullptr;
     if (int st = ensure_workspace(m, s, rows, &w)) return st;
     const int L = m->L;
-    const int tile = choose_tile(m, rows);
+    const Tile tile = choose_tile(m, rows);
     // Small per-call tables: rows' request ids, request offsets, exit state.
     std::vector<int> row_req(rows);
     for (int r = 0; r < requests; ++r)

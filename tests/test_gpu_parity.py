@@ -62,10 +62,10 @@ def test_16bit_operands(oracle, dtype, act):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("tile", [64, 128, 256])
+@pytest.mark.parametrize("tile", [(64, 64), (128, 128), (256, 128), (256, 256)])
 def test_every_tile_shape(oracle, dtype, tile):
     snap, W, b, P, x = build_case([300, 260, 200], "tanh", 0.1, batch=300, seed=7, bias_scale=0.1)
-    top, _, en = run_gpu(snap, x, 6, dtype=dtype, energy=True, options={"tile": tile})
+    top, _, en = run_gpu(snap, x, 6, dtype=dtype, energy=True, options={"tile": tile[0], "tile_n": tile[1]})
     rtop, _, ren = run_oracle(oracle, snap, W, b, P, x, 6, dtype=dtype, energy=True)
     tol = 1e-4 if dtype == "f32" else 2e-3
     errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren))
