@@ -1,34 +1,71 @@
-"""Ahead-of-time build of libpcdevice_hip.so for gfx950 (no JIT, no cache outside the tree)."""
+"""Ahead-of-time build of libpcdevice_hip.so for gfx950 (no JIT, no cache outside the tree).
+
+The library is one host translation unit (csrc/pcdevice.hip) plus one unit per
+(operand type, GEMM tile) instantiation of the phase kernels
+(csrc/phase_inst.hip compiled with -DPCD_OP_ID/-DPCD_BM/-DPCD_BN); the units
+compile in parallel and link into one shared object.
+"""
 from __future__ import annotations
 
 import os
 import subprocess
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libpcdevice_hip.so")
-SOURCES = [os.path.join(HERE, "csrc", "pcdevice.hip")]
-DEPENDS = SOURCES + [os.path.join(HERE, "csrc", "pc_kernels.hpp"), os.path.join(ROOT, "include", "pcdevice.h")]
+HOST_SOURCE = os.path.join(CSRC, "pcdevice.hip")
+INST_SOURCE = os.path.join(CSRC, "phase_inst.hip")
+
+OPS = {"f32": 0, "bf16": 1, "f16": 2}
+TILES = [(64, 64), (128, 128), (256, 128), (256, 256)]
 
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # no packed-fp32 instructions: some of their forms have misbehaved on this pool
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-result",
 ]
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile the HIP library in-tree (always recompiles)."""
-    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB + ".tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, *SOURCES, "-o", tmp]
+def _units():
+    """(source, extra flags, object name) of every translation unit."""
+    units = [(HOST_SOURCE, [], "pcdevice.o")]
+    for op, op_id in OPS.items():
+        for bm, bn in TILES:
+            units.append((INST_SOURCE, [f"-DPCD_OP_ID={op_id}", f"-DPCD_BM={bm}", f"-DPCD_BN={bn}"],
+                          f"phase_{op}_{bm}x{bn}.o"))
+    return units
+
+
+def _run(cmd):
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
-    if verbose and out.strip():
-        print(out)
+    return res.returncode, out
+
+
+def build_library(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile the HIP library in-tree (always recompiles every unit)."""
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    with tempfile.TemporaryDirectory(prefix="pcd_build_") as tmpdir:
+        units = _units()
+        cmds = [[hipcc, *HIPCC_FLAGS, *flags, "-c", src, "-o", os.path.join(tmpdir, obj)]
+                for src, flags, obj in units]
+        with ThreadPoolExecutor(jobs) as ex:
+            results = list(ex.map(_run, cmds))
+        for (src, flags, obj), (rc, out) in zip(units, results):
+            if rc != 0:
+                raise RuntimeError(f"hipcc failed on {obj} ({rc}):\n{out}")
+            if verbose and out.strip():
+                print(out)
+        tmp = LIB + ".tmp"
+        rc, out = _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC",
+                        *[os.path.join(tmpdir, obj) for _, _, obj in units], "-o", tmp])
+        if rc != 0:
+            raise RuntimeError(f"link failed ({rc}):\n{out}")
     os.replace(tmp, LIB)
     return LIB
 

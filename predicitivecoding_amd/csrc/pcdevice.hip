@@ -21,7 +21,8 @@
 #include <vector>
 
 #include "../../include/pcdevice.h"
-#include "pc_kernels.hpp"
+#include "aux_kernels.hpp"
+#include "phase_launch.hpp"
 
 using namespace pcd;
 
@@ -147,13 +148,7 @@ int pool_free(void* ptr, hipStream_t stream) {
 
 template <typename OP, int BM, int BN>
 int launch_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
-    switch (epi) {
-    case EPI_ERROR: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_ERROR>), dim3(grid), dim3(256), 0, s, set, args); break;
-    case EPI_UPDATE: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_UPDATE>), dim3(grid), dim3(256), 0, s, set, args); break;
-    case EPI_FFG: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_FFG>), dim3(grid), dim3(256), 0, s, set, args); break;
-    default: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN>), dim3(grid), dim3(256), 0, s, set, args); break;
-    }
-    return from_hip(hipGetLastError(), "phase_kernel launch");
+    return from_hip(launch_phase_tile<OP, BM, BN>(epi, set, args, grid, s), "phase_kernel launch");
 }
 
 // GEMM tile shapes compiled into the library (rows x columns of the output).

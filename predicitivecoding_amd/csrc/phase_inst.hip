@@ -1,0 +1,37 @@
+// phase_inst.hip -- one (operand type, tile) instantiation of the phase kernels.
+//
+// Compiled once per combination with
+//   -DPCD_OP_ID=0|1|2   (fp32, bf16, fp16 operands)
+//   -DPCD_BM=64|128|256 -DPCD_BN=64|128|256
+// and linked into libpcdevice_hip.so next to pcdevice.hip.
+#include "phase_launch.hpp"
+
+#if !defined(PCD_OP_ID) || !defined(PCD_BM) || !defined(PCD_BN)
+#error "phase_inst.hip needs PCD_OP_ID, PCD_BM and PCD_BN"
+#endif
+
+namespace pcd {
+
+#if PCD_OP_ID == 0
+typedef float InstOp;
+#elif PCD_OP_ID == 1
+typedef bf16_t InstOp;
+#else
+typedef f16_t InstOp;
+#endif
+
+template <typename OP, int BM, int BN>
+hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
+    switch (epi) {
+    case EPI_ERROR: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_ERROR>), dim3(grid), dim3(256), 0, s, set, args); break;
+    case EPI_UPDATE: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_UPDATE>), dim3(grid), dim3(256), 0, s, set, args); break;
+    case EPI_FFG: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_FFG>), dim3(grid), dim3(256), 0, s, set, args); break;
+    default: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN>), dim3(grid), dim3(256), 0, s, set, args); break;
+    }
+    return hipGetLastError();
+}
+
+template hipError_t launch_phase_tile<InstOp, PCD_BM, PCD_BN>(int, const ProblemSet&, const PhaseArgs&, int,
+                                                              hipStream_t);
+
+}  // namespace pcd

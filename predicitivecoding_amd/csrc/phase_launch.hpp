@@ -1,0 +1,33 @@
+// phase_launch.hpp -- host-side entry to the phase kernels.
+//
+// Each (operand type, tile) instantiation of phase_kernel lives in its own
+// translation unit (phase_inst.hip compiled once per combination), so the
+// library's kernels build in parallel.  The host code calls them through this
+// declaration; the definitions are explicit instantiations in those units.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "pc_kernels.hpp"
+
+namespace pcd {
+
+// Launches phase_kernel<OP, BM, BN, epi> over `grid` workgroups of 256 threads
+// on `stream` and returns the launch status.
+template <typename OP, int BM, int BN>
+hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t stream);
+
+#define PCD_DECLARE_TILE(OP, BM, BN)                                                                    \
+    extern template hipError_t launch_phase_tile<OP, BM, BN>(int, const ProblemSet&, const PhaseArgs&, int, \
+                                                             hipStream_t);
+#define PCD_DECLARE_OP(OP)         \
+    PCD_DECLARE_TILE(OP, 64, 64)   \
+    PCD_DECLARE_TILE(OP, 128, 128) \
+    PCD_DECLARE_TILE(OP, 256, 128) \
+    PCD_DECLARE_TILE(OP, 256, 256)
+PCD_DECLARE_OP(float)
+PCD_DECLARE_OP(bf16_t)
+PCD_DECLARE_OP(f16_t)
+#undef PCD_DECLARE_OP
+#undef PCD_DECLARE_TILE
+
+}  // namespace pcd
