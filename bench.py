@@ -78,15 +78,20 @@ def cpu_baseline(cfg, W, b, x_host, budget_s=10.0):
     pc_oracle.set_threads(threads)
     sizes, act = cfg["sizes"], ACT_NAME[cfg["act"]]
     P = [1.0] * len(sizes)
-    # calibrate on one step of a small slice, then size the sample to the budget
+    # calibrate on one step of a small slice (after one untimed call that
+    # starts the thread pool and warms the caches), then size the sample to
+    # the budget
     rows = min(cfg["batch"], max(4 * threads, 16))
-    t0 = time.perf_counter()
     pc_oracle.batched_relax(sizes, act, cfg["eta"], W, b, P, x_host[:rows], 1)
-    per = (time.perf_counter() - t0) / rows
+    t0 = time.perf_counter()
+    pc_oracle.batched_relax(sizes, act, cfg["eta"], W, b, P, x_host[:rows], 2)
+    per = (time.perf_counter() - t0) / (2 * rows)
     steps = int(max(1, min(cfg["T"], budget_s / max(per * rows, 1e-9))))
     if steps == cfg["T"]:
         rows = int(max(rows, min(cfg["batch"], budget_s / max(per * cfg["T"], 1e-9))))
         rows = min(rows, cfg["batch"])
+    print(f"# cpu baseline sample: {rows} rows x {steps} steps (calibrated {per * 1e3:.3f} ms per "
+          f"sample-step)", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
     pc_oracle.batched_relax(sizes, act, cfg["eta"], W, b, P, x_host[:rows], steps)
     dt = time.perf_counter() - t0
@@ -95,15 +100,92 @@ def cpu_baseline(cfg, W, b, x_host, budget_s=10.0):
                       f"{rows} of {cfg['batch']} samples x {steps} of {cfg['T']} steps, {dt:.1f} s"}
 
 
-def traffic_from_profiles(workload):
+def traffic_from_profiles(workload, kernel):
+    """HBM bytes per launch of `kernel` ("error_phase" / "update_phase") from
+    the committed PMC summary profiles/traffic_<workload>.json (written by
+    --traffic-from), or None when it has not been measured."""
     path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
     if not os.path.exists(path):
         return None
     try:
         with open(path) as f:
-            return json.load(f).get("bytes_per_launch")
-    except (OSError, ValueError):
+            return json.load(f)["kernels"][kernel]["bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
         return None
+
+
+COPY_CALIB_BYTES = 1 << 30
+
+
+def calibrate_copy():
+    """One elementwise copy of COPY_CALIB_BYTES (torch.mul by 1 into a new
+    tensor: reads and writes exactly that many bytes).  Profiled with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, it gives the factor between the
+    counters and real bytes."""
+    import torch
+    x = torch.ones(COPY_CALIB_BYTES // 4, device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+    y = torch.mul(x, 1.0)
+    torch.cuda.synchronize()
+    print(f"# copy calibration: {COPY_CALIB_BYTES} bytes read and written ({float(y[0])})", file=sys.stderr)
+
+
+def _pmc_rows(directory):
+    """Rows of every rocprofv3 counter_collection.csv under `directory`."""
+    import csv
+    import glob
+    rows = []
+    for path in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            rows.extend(csv.DictReader(f))
+    if not rows:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    return rows
+
+
+def _mean_counter(rows, counter, name_filter):
+    """Mean per dispatch of `counter` over the dispatches whose kernel name
+    passes name_filter (a counter's per-dispatch value is the sum of its
+    instance rows)."""
+    per_dispatch = {}
+    for r in rows:
+        if r.get("Counter_Name") != counter or not name_filter(r.get("Kernel_Name", "")):
+            continue
+        key = r.get("Dispatch_Id") or r.get("Correlation_Id")
+        per_dispatch[key] = per_dispatch.get(key, 0.0) + float(r["Counter_Value"])
+    if not per_dispatch:
+        raise SystemExit(f"no {counter} rows for the requested kernel")
+    return sum(per_dispatch.values()) / len(per_dispatch), len(per_dispatch)
+
+
+def traffic_from_pmc(workload, fetch_dir, write_dir, calib_fetch_dir, calib_write_dir, command):
+    """Writes profiles/traffic_<workload>.json: HBM bytes per launch of each
+    phase kernel from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each
+    scaled by what the same counter reads for the calibration copy."""
+    is_copy = lambda n: "MulFunctor" in n
+    cf, _ = _mean_counter(_pmc_rows(calib_fetch_dir), "FETCH_SIZE", is_copy)
+    cw, _ = _mean_counter(_pmc_rows(calib_write_dir), "WRITE_SIZE", is_copy)
+    f_fetch = cf * 1024.0 / COPY_CALIB_BYTES
+    f_write = cw * 1024.0 / COPY_CALIB_BYTES
+    fr, wr = _pmc_rows(fetch_dir), _pmc_rows(write_dir)
+    out = {"workload": workload, "command": command,
+           "calibration": {"bytes": COPY_CALIB_BYTES, "fetch_kib": cf, "write_kib": cw,
+                           "fetch_factor": f_fetch, "write_factor": f_write},
+           "kernels": {}}
+    for name, tag in (("error_phase", ", 0>"), ("update_phase", ", 1>")):
+        sel = lambda n, tag=tag: "phase_kernel" in n and n.rstrip().endswith(tag + "(pcd::ProblemSet, pcd::PhaseArgs)")
+        fk, nf = _mean_counter(fr, "FETCH_SIZE", sel)
+        wk, nw = _mean_counter(wr, "WRITE_SIZE", sel)
+        fetch_b = fk * 1024.0 / f_fetch
+        write_b = wk * 1024.0 / f_write
+        out["kernels"][name] = {"fetch_kib": fk, "write_kib": wk, "dispatches": [nf, nw],
+                                "fetch_bytes": fetch_b, "write_bytes": write_b,
+                                "bytes_per_launch": fetch_b + write_b}
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out, indent=1))
 
 
 def main():
@@ -116,11 +198,23 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--tile", type=int, default=0, help="force the GEMM tile rows (and columns unless --tile-n)")
     ap.add_argument("--tile-n", type=int, default=0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only the copy kernel that calibrates FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "CALIB_FETCH_DIR", "CALIB_WRITE_DIR"),
+                    help="derive profiles/traffic_<config>.json from rocprofv3 --pmc output directories")
+    ap.add_argument("--traffic-command", default="", help="command line recorded with --traffic-from")
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_from_pmc(args.config, *args.traffic_from, args.traffic_command)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build runs the relaxation on a single MI355X "
               "(the batch shards over GPUs with no per-step communication; see DESIGN.md).", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     import torch
     from predicitivecoding_amd import GenerativeSnapshot, PcDeviceModel
@@ -175,7 +269,7 @@ def main():
     achieved = flop_launch / (dom_ms * 1e-3)
     peak = PEAK[cfg["dtype"]]
     roofline = {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
-                "frac": achieved / peak, "traffic": traffic_from_profiles(args.config),
+                "frac": achieved / peak, "traffic": traffic_from_profiles(args.config, dom_name),
                 "kernel": dom_name, "kernel_ms": dom_ms, "error_phase_ms": err_ms, "update_phase_ms": upd_ms,
                 "flop_per_launch": flop_launch, "launches_timed": launches,
                 "path_frac": (flops_per_sample_step(sizes) * value) / peak}

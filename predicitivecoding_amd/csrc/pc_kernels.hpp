@@ -20,11 +20,14 @@
 // The two phases are the Jacobi order of Network.cs:91-110: every error is
 // computed from the pre-step states before any state moves.
 //
-// Tiling: a 256-thread workgroup (4 waves, 2 x 2) owns a BM x BN output tile;
-// each wave owns (BM/2) x (BN/2) as 32 x 32 MFMA blocks.  K advances in
-// stages of 128 bytes per row staged through LDS (double buffered, one
-// barrier per stage), 16-byte units XOR-swizzled by row so that the 16-byte
-// fragment reads of a wave hit distinct banks.
+// Tiling: a workgroup owns a BM x BN output tile; its waves (2 x 2, or 2 x 4
+// for 256 x 256) each own a (BM/WM) x (BN/WN) part as 32 x 32 MFMA blocks.
+// K advances in stages of 64 or 128 bytes per row, copied global -> LDS
+// directly (no register staging) a few stages ahead, one barrier per stage;
+// 16-byte units are XOR-swizzled by row so that the 16-byte fragment reads of
+// a wave hit distinct banks.  The fragment reads of the next 32-byte chunk
+// are interleaved with the MFMAs of the current one.  The epilogues keep the
+// operands of the next few 32 x 32 blocks in flight while a block computes.
 //   16-bit operands: v_mfma_f32_32x32x16_{bf16,f16}; lane l holds 8 consecutive
 //     K values of row (l % 32), half-wave l/32 takes the second 8 of each 16.
 //   fp32 operands:   v_mfma_f32_32x32x2f32 x 4 per 32-byte chunk: lane l holds 4
@@ -224,34 +227,45 @@ __device__ __forceinline__ bool row_active(const PhaseArgs& a, int row) {
     return a.row_req == nullptr || a.t < a.done_at[a.row_req[row]];
 }
 
-// LDS layout of one pipeline stage: rows of kRowBytes (the K slice of one
-// A or B row), A rows first, then B rows.  The four 16-byte units of row R sit
-// at unit u ^ ((R >> 2) & 3).  Measured on gfx950 with SQ_LDS_BANK_CONFLICT,
-// this makes the fragment reads (32 consecutive rows x 2 units per wave, one
-// ds_read_b128 each) conflict-free; XOR keys built from other row bits leave
-// a 2-way conflict.
-constexpr int kRowBytes = 64;                 // K bytes per row per stage
-constexpr int kUnits = kRowBytes / 16;        // 16-byte units per row
-__device__ __forceinline__ int swz(int row, int unit) { return unit ^ ((row >> 2) & 3); }
+// LDS layout of one pipeline stage: rows of RB bytes (the K slice of one A or
+// B row), A rows first, then B rows.  The 16-byte units of row R are stored
+// permuted, unit u at u ^ ((R / (256 / RB)) % (RB / 16)): consecutive rows
+// then cover all 64 four-byte banks (256 bytes) before a bank repeats, so the
+// fragment reads (32 consecutive rows x 2 units per wave, one ds_read_b128
+// each) are conflict-free.  For 64-byte rows this was measured on gfx950 with
+// SQ_LDS_BANK_CONFLICT (zero); XOR keys built from other row bits leave a
+// 2-way conflict.
+template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
+    return unit ^ ((row / (256 / RB)) % (RB / 16));
+}
 
 template <int BM, int BN> struct TileCfg {
-    static constexpr int WM = 2, WN = 2;
+    // 256 x 256 runs 8 waves (2 x 4 of 128 x 64: two waves per SIMD share the
+    // MFMA pipe) over 128-byte K stages, double buffered (128 KB of LDS, one
+    // workgroup per CU).  The other tiles run 4 waves (2 x 2) over 64-byte
+    // stages; 256 x 128 keeps 3 stages (72 KB) so two workgroups fit a CU.
+    static constexpr bool BIG = BM == 256 && BN == 256;
+    static constexpr int WM = 2, WN = BIG ? 4 : 2;
+    static constexpr int NWAVES = WM * WN, NT = 64 * NWAVES;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
-    static constexpr int stage_bytes = (BM + BN) * kRowBytes;
-    // Stages in the LDS ring: 4 (prefetch distance 3) unless that would keep
-    // a second workgroup off the CU; 256 x 128 runs 3 stages (72 KB) so two
-    // workgroups share a CU and one's epilogue overlaps the other's MFMAs.
-    static constexpr int NS = (BM == 256 && BN == 128) ? 3 : 4;
-    static constexpr int D = NS - 1;                      // prefetch distance (stages)
-    // Workgroups per CU the register budget is sized for (256 x 256 needs the
-    // whole register file of a SIMD for its 256 accumulators per lane).
-    static constexpr int OCC = (BM == 256 && BN == 256) ? 1 : 2;
-    static constexpr int ROWS_PER_LOAD = 64 * 16 / kRowBytes;             // rows one wave-wide load fills
-    static constexpr int QPW = (BM + BN) / ROWS_PER_LOAD / 4;             // loads per wave per stage
+    static constexpr int RB = BIG ? 128 : 64;              // K bytes per row per stage
+    static constexpr int UNITS = RB / 16;                  // 16-byte units per row
+    static constexpr int NC = RB / 32;                     // 32-byte MFMA chunks per stage
+    static constexpr int stage_bytes = (BM + BN) * RB;
+    static constexpr int NS = BIG ? 2 : (BM == 256 && BN == 128) ? 3 : 4;   // stages in the LDS ring
+    static constexpr int D = NS - 1;                       // prefetch distance (stages)
+    static constexpr int OCC = BIG ? 1 : 2;                // workgroups per CU the registers are sized for
+    static constexpr int ROWS_PER_LOAD = 64 * 16 / RB;     // rows one wave-wide 16-byte-per-lane load fills
+    static constexpr int QPW = (BM + BN) / ROWS_PER_LOAD / NWAVES;   // loads per wave per stage
     static_assert(FM >= 1 && FN >= 1 && QPW >= 1, "tile too small");
-    static_assert((BM + BN) % (4 * ROWS_PER_LOAD) == 0, "stage rows must split evenly over 4 waves");
+    static_assert((BM + BN) % (NWAVES * ROWS_PER_LOAD) == 0, "stage rows must split evenly over the waves");
+    static_assert(NC % 2 == 0, "fragment buffers alternate within a stage");
+    static_assert(D >= 1 && D <= 3, "stage_ready handles prefetch distances 1 to 3");
 };
+
+// Energy partial slots one tile column owns (one per wave column).
+template <int BM, int BN> constexpr int energy_slots_per_tile_n() { return TileCfg<BM, BN>::WN; }
 
 // Direct global -> LDS copy of 16 bytes per lane (gfx950 global_load_lds_dwordx4):
 // lane l's bytes land at LDS address m0 + 16 l.  Issued as inline asm so the
@@ -260,7 +274,7 @@ template <int BM, int BN> struct TileCfg {
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_addr) : "memory", "m0");
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_addr) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
@@ -271,7 +285,7 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <typename OP, int BM, int BN, int EPI>
-__global__ void __launch_bounds__(256, (TileCfg<BM, BN>::OCC))
+__global__ void __launch_bounds__((TileCfg<BM, BN>::NT), (TileCfg<BM, BN>::OCC))
 phase_kernel(const ProblemSet set, const PhaseArgs args) {
     using C = TileCfg<BM, BN>;
     constexpr int OPB = OpTraits<OP>::bytes;
@@ -284,7 +298,7 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     // Energy of the previous error phase, reduced per row in a fixed order
     // before any tile work (deterministic, no atomics).
     if (EPI == EPI_UPDATE && args.energy_out != nullptr) {
-        for (int row = blockIdx.x * 256 + tid; row < args.batch; row += gridDim.x * 256) {
+        for (int row = blockIdx.x * C::NT + tid; row < args.batch; row += gridDim.x * C::NT) {
             float s = 0.f;
             for (int k = 0; k < args.nslots; ++k) s += args.energy_part[(size_t)k * args.ldp + row];
             args.energy_out[(size_t)args.t * args.batch + row] = s;
@@ -327,26 +341,26 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     const char* Ag = (const char*)P.A + (size_t)row0 * P.lda * OPB;
     const char* Bg = (const char*)P.B + (size_t)col0 * P.ldb * OPB;
     const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
-    constexpr int KE = kRowBytes / OPB;  // K elements per stage
+    constexpr int KE = C::RB / OPB;  // K elements per stage
     const int nk = P.K / KE;
 
     // This lane's source of each of its wave's QPW loads per stage: combined
-    // stage row R = q*ROWS_PER_LOAD + lane/4 (A rows, then B rows), physical
-    // unit lane%4, which holds logical unit swz(R, lane%4).
+    // stage row R = q*ROWS_PER_LOAD + lane/UNITS (A rows, then B rows),
+    // physical unit lane%UNITS, which holds logical unit swz(R, lane%UNITS).
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const char* src[C::QPW];
 #pragma unroll
     for (int i = 0; i < C::QPW; ++i) {
         const int q = wave_u * C::QPW + i;
-        const int R = q * C::ROWS_PER_LOAD + (lane >> 2);
-        const int unit = swz(R, lane & 3);
+        const int R = q * C::ROWS_PER_LOAD + lane / C::UNITS;
+        const int unit = swz<C::RB>(R, lane % C::UNITS);
         src[i] = R < BM ? Ag + (size_t)R * lda_b + unit * 16 : Bg + (size_t)(R - BM) * ldb_b + unit * 16;
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
     auto issue_stage = [&](int kt) PCD_INLINE {
         const uint32_t base = lds0 + (kt % C::NS) * C::stage_bytes + wave_u * C::QPW * 1024;
 #pragma unroll
-        for (int i = 0; i < C::QPW; ++i) lds_dma16(src[i] + (size_t)kt * kRowBytes, base + i * 1024);
+        for (int i = 0; i < C::QPW; ++i) lds_dma16(src[i] + (size_t)kt * C::RB, base + i * 1024);
     };
     // Fragments of K chunk c (32 bytes per row) of the stage in `slot`.
     const int half = lane >> 5, lr = lane & 31;
@@ -355,12 +369,12 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
 #pragma unroll
         for (int i = 0; i < C::FM; ++i) {
             const int R = wm * C::WTM + i * 32 + lr;
-            a[i] = *(const u32x4*)(st + R * kRowBytes + swz(R, 2 * c + half) * 16);
+            a[i] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
         }
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) {
             const int R = BM + wn * C::WTN + j * 32 + lr;
-            b[j] = *(const u32x4*)(st + R * kRowBytes + swz(R, 2 * c + half) * 16);
+            b[j] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
         }
     };
     auto mfmas = [&](const u32x4* a, const u32x4* b) PCD_INLINE {
@@ -378,112 +392,156 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
             if (later >= 2) wait_vmcnt<2 * C::QPW>();
             else if (later == 1) wait_vmcnt<C::QPW>();
             else wait_vmcnt<0>();
-        } else {
+        } else if constexpr (C::D == 2) {
             if (later >= 1) wait_vmcnt<C::QPW>();
             else wait_vmcnt<0>();
+        } else {
+            wait_vmcnt<0>();
         }
         __syncthreads();
     };
-
-    u32x4 fa0[C::FM], fb0[C::FN], fa1[C::FM], fb1[C::FN];
-    static_assert(C::D == 2 || C::D == 3, "stage_ready handles prefetch distances 2 and 3");
+    constexpr int NC = C::NC;
+    u32x4 fa[2][C::FM], fb[2][C::FN];
+    auto interleave = [&]() PCD_INLINE {
+        static_for<0, C::FM + C::FN>([&](auto) PCD_INLINE {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        });
+        __builtin_amdgcn_sched_group_barrier(0x008, C::FM * C::FN - (C::FM + C::FN), 0);
+    };
     for (int s2 = 0; s2 < C::D && s2 < nk; ++s2) issue_stage(s2);
     stage_ready(0);
-    read_frags(0, 0, fa0, fb0);
-    // Steady state: the next stage's first fragments are read right after the
-    // barrier and consumed one MFMA group later.  The last stage is peeled off
-    // so no path through the loop skips those reads (a merge there makes the
-    // compiler wait for them before the second group).
+    read_frags(0, 0, fa[0], fb[0]);
+    // Chunk c's MFMAs run while chunk c+1's fragments are read; the last chunk
+    // of a stage runs after the barrier that publishes the next stage, whose
+    // first fragments it overlaps.  The last stage is peeled off.
     for (int kt = 0; kt + 1 < nk; ++kt) {
         if (kt + C::D < nk) issue_stage(kt + C::D);
-        read_frags(kt % C::NS, 1, fa1, fb1);
-        mfmas(fa0, fb0);
-        stage_ready(kt + 1);
-        read_frags((kt + 1) % C::NS, 0, fa0, fb0);
-        mfmas(fa1, fb1);
+        static_for<0, NC>([&](auto Cc) PCD_INLINE {
+            constexpr int c = decltype(Cc)::value;
+            if constexpr (c + 1 < NC) {
+                read_frags(kt % C::NS, c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
+            } else {
+                stage_ready(kt + 1);
+                read_frags((kt + 1) % C::NS, 0, fa[0], fb[0]);
+            }
+            mfmas(fa[c & 1], fb[c & 1]);
+            interleave();
+        });
     }
-    read_frags((nk - 1) % C::NS, 1, fa1, fb1);
-    mfmas(fa0, fb0);
-    mfmas(fa1, fb1);
+    static_for<0, NC>([&](auto Cc) PCD_INLINE {
+        constexpr int c = decltype(Cc)::value;
+        if constexpr (c + 1 < NC) read_frags((nk - 1) % C::NS, c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
+        mfmas(fa[c & 1], fb[c & 1]);
+    });
 
     // ---- epilogue
     // Row of register r of a block in row-block i: 8*(r/4) + 4*half + r%4.
     auto row_of = [&](int i, int r) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
     auto col_of = [&](int j) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + lr; };
     if constexpr (EPI == EPI_ERROR) {
+        // Blocks b = i*FN + j in order; the M_{l-1} operands of the next PD
+        // blocks are in flight while a block computes, so the load latency is
+        // paid about once per tile instead of once per block.
+        constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
         const float P_low = P.prec, inv2p = 0.5f / P.prec;
         const bool want_energy = args.energy_part != nullptr;
-        static_for<0, C::FM>([&](auto I) PCD_INLINE {
-            constexpr int i = decltype(I)::value;
-            float esum[16];
-            static_for<0, 16>([&](auto R) PCD_INLINE { esum[decltype(R)::value] = 0.f; });
-            static_for<0, C::FN>([&](auto J) PCD_INLINE {
-                constexpr int j = decltype(J)::value;
-                __builtin_amdgcn_sched_barrier(0);  // keep each block's epilogue to itself
-                const int col = col_of(j);
-                const bool cok = col < P.N;
-                const float bj = cok ? P.bias[col] : 0.f;
+        float mv[PD][16];
+        float esum[16];
+        auto load_block = [&](auto Bc) PCD_INLINE {
+            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+            const int col = col_of(j);
+            static_for<0, 16>([&](auto R) PCD_INLINE {
+                constexpr int r = decltype(R)::value;
+                const int row = row_of(i, r);
+                mv[b % PD][r] = (col < P.N && row < P.M) ? P.mlow[(size_t)row * P.ldo + col] : 0.f;
+            });
+        };
+        static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
+        static_for<0, NB>([&](auto Bc) PCD_INLINE {
+            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+            if constexpr (j == 0) static_for<0, 16>([&](auto R) PCD_INLINE { esum[decltype(R)::value] = 0.f; });
+            const int col = col_of(j);
+            const bool cok = col < P.N;
+            const float bj = cok ? P.bias[col] : 0.f;
+            static_for<0, 16>([&](auto R) PCD_INLINE {
+                constexpr int r = decltype(R)::value;
+                const int row = row_of(i, r);
+                if (cok && row < P.M && row_active(args, row)) {
+                    const size_t idx = (size_t)row * P.ldo + col;
+                    const float pre = acc[i][j][r] + bj;
+                    float y, dy;
+                    act_eval(args.act, pre, y, dy);
+                    const float e = P_low * (mv[b % PD][r] - y);
+                    const float d = dy * e;
+                    OpTraits<OP>::store(P.dout, idx, d);
+                    if (P.eout) P.eout[idx] = e;
+                    esum[r] += e * e * inv2p;
+                }
+            });
+            if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
+            if constexpr (j == C::FN - 1) {
+                if (want_energy) {
+                    static_for<0, 16>([&](auto R) PCD_INLINE {
+                        constexpr int r = decltype(R)::value;
+                        float v = esum[r];
+                        v += __shfl_xor(v, 16);
+                        v += __shfl_xor(v, 8);
+                        v += __shfl_xor(v, 4);
+                        v += __shfl_xor(v, 2);
+                        v += __shfl_xor(v, 1);
+                        esum[r] = v;
+                    });
+                    if (lr == 0) {
+                        const int slot = P.slot_base + tn * C::WN + wn;
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            const int row = row_of(i, r);
+                            if (row < P.M) args.energy_part[(size_t)slot * args.ldp + row] = esum[r];
+                        });
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // the next block starts after this one's loads are issued
+        });
+    } else if constexpr (EPI == EPI_UPDATE) {
+        // As the error epilogue: M_l and E_l of the next PD blocks in flight.
+        constexpr int NB = C::FM * C::FN, PD = NB < 2 ? NB : 2;
+        const float eta = args.eta, lam = args.act_reg;
+        float mv[PD][16], ev[PD][16];
+        auto load_block = [&](auto Bc) PCD_INLINE {
+            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+            const int col = col_of(j);
+            static_for<0, 16>([&](auto R) PCD_INLINE {
+                constexpr int r = decltype(R)::value;
+                const int row = row_of(i, r);
+                const bool ok = col < P.N && row < P.M;
+                const size_t idx = (size_t)row * P.ldo + col;
+                mv[b % PD][r] = ok ? P.m[idx] : 0.f;
+                ev[b % PD][r] = ok && P.eself ? P.eself[idx] : 0.f;
+            });
+        };
+        static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
+        static_for<0, NB>([&](auto Bc) PCD_INLINE {
+            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+            const int col = col_of(j);
+            if (col < P.N) {
                 static_for<0, 16>([&](auto R) PCD_INLINE {
                     constexpr int r = decltype(R)::value;
                     const int row = row_of(i, r);
-                    if (cok && row < P.M && row_active(args, row)) {
+                    if (row < P.M && row_active(args, row)) {
                         const size_t idx = (size_t)row * P.ldo + col;
-                        const float pre = acc[i][j][r] + bj;
-                        float y, dy;
-                        act_eval(args.act, pre, y, dy);
-                        const float e = P_low * (P.mlow[idx] - y);
-                        const float d = dy * e;
-                        OpTraits<OP>::store(P.dout, idx, d);
-                        if (P.eout) P.eout[idx] = e;
-                        esum[r] += e * e * inv2p;
+                        float m = mv[b % PD][r];
+                        float grad = ev[b % PD][r] - acc[i][j][r];
+                        if (lam > 0.f) grad += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
+                        m -= eta * grad;
+                        P.m[idx] = m;
+                        if (P.mop) OpTraits<OP>::store(P.mop, idx, m);
                     }
                 });
-            });
-            if (want_energy) {
-                static_for<0, 16>([&](auto R) PCD_INLINE {
-                    constexpr int r = decltype(R)::value;
-                    float v = esum[r];
-                    v += __shfl_xor(v, 16);
-                    v += __shfl_xor(v, 8);
-                    v += __shfl_xor(v, 4);
-                    v += __shfl_xor(v, 2);
-                    v += __shfl_xor(v, 1);
-                    esum[r] = v;
-                });
-                if (lr == 0) {
-                    const int slot = P.slot_base + tn * C::WN + wn;
-                    static_for<0, 16>([&](auto R) PCD_INLINE {
-                        constexpr int r = decltype(R)::value;
-                        const int row = row_of(i, r);
-                        if (row < P.M) args.energy_part[(size_t)slot * args.ldp + row] = esum[r];
-                    });
-                }
             }
-        });
-    } else if constexpr (EPI == EPI_UPDATE) {
-        const float eta = args.eta, lam = args.act_reg;
-        static_for<0, C::FM>([&](auto I) PCD_INLINE {
-            constexpr int i = decltype(I)::value;
-            static_for<0, C::FN>([&](auto J) PCD_INLINE {
-                constexpr int j = decltype(J)::value;
-                __builtin_amdgcn_sched_barrier(0);  // keep each block's epilogue to itself
-                const int col = col_of(j);
-                if (col < P.N) {
-                    static_for<0, 16>([&](auto R) PCD_INLINE {
-                        constexpr int r = decltype(R)::value;
-                        const int row = row_of(i, r);
-                        if (row < P.M && row_active(args, row)) {
-                            const size_t idx = (size_t)row * P.ldo + col;
-                            float m = P.m[idx];
-                            float grad = (P.eself ? P.eself[idx] : 0.f) - acc[i][j][r];
-                            if (lam > 0.f) grad += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
-                            m -= eta * grad;
-                            P.m[idx] = m;
-                            if (P.mop) OpTraits<OP>::store(P.mop, idx, m);
-                        }
-                    });
-                }
-            });
+            if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
+            __builtin_amdgcn_sched_barrier(0);
         });
     } else if constexpr (EPI == EPI_FFG) {
         static_for<0, C::FM>([&](auto I) PCD_INLINE {

@@ -272,14 +272,31 @@ Tile choose_tile(const pcd_model* m, int batch) {
     if (m->dtype != PCD_F32 && batch >= 1024) {
         bool wide = true;
         for (int l = 0; l < m->L; ++l) wide = wide && m->s[l] >= 1024;
-        if (wide) return Tile{256, 128};
+        if (wide) return Tile{256, 256};
     }
     return Tile{128, 128};
 }
 
-int energy_slots(const pcd_model* m, int tile_n) {
+// Energy partial slots a tile column owns: one per wave column of the tile.
+int slots_per_tile_n(Tile t) {
+    if (t.m == 256 && t.n == 256) return energy_slots_per_tile_n<256, 256>();
+    if (t.m == 256 && t.n == 128) return energy_slots_per_tile_n<256, 128>();
+    if (t.m == 128 && t.n == 128) return energy_slots_per_tile_n<128, 128>();
+    return energy_slots_per_tile_n<64, 64>();
+}
+
+// Energy partial slots of one step with `tile`.
+int energy_slots(const pcd_model* m, Tile tile) {
     int slots = 0;
-    for (int l = 1; l < m->L; ++l) slots += (int)((m->s[l - 1] + tile_n - 1) / tile_n) * 2;
+    for (int l = 1; l < m->L; ++l) slots += (int)((m->s[l - 1] + tile.n - 1) / tile.n) * slots_per_tile_n(tile);
+    return slots;
+}
+
+// The most slots any supported tile needs (sizes the workspace once).
+int max_energy_slots(const pcd_model* m) {
+    const Tile tiles[] = {{64, 64}, {128, 128}, {256, 128}, {256, 256}};
+    int slots = 0;
+    for (Tile t : tiles) slots = std::max(slots, energy_slots(m, t));
     return slots;
 }
 
@@ -293,7 +310,7 @@ int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out
         w->stream = stream;
     }
     int need = (int)round_up((size_t)std::max(rows, 1), kRowPad);
-    int slots = energy_slots(m, 64);  // the narrowest tile has the most slots
+    int slots = max_energy_slots(m);
     if (w->cap >= need && w->slots_cap >= slots) {
         *out = w;
         return PCD_SUCCESS;
@@ -361,7 +378,7 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         p.dout = w->D[l];
         p.prec = m->prec[l - 1];
         p.slot_base = slot;
-        slot += p.tiles_n * 2;
+        slot += p.tiles_n * slots_per_tile_n(tile);
     }
     for (int l = 1; l < L; ++l) {
         if (upd.empty() || upd.back().n == kMaxProblems) { upd.emplace_back(); upd.back().n = 0; }

@@ -22,11 +22,12 @@ typedef f16_t InstOp;
 
 template <typename OP, int BM, int BN>
 hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
+    const dim3 block(TileCfg<BM, BN>::NT);
     switch (epi) {
-    case EPI_ERROR: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_ERROR>), dim3(grid), dim3(256), 0, s, set, args); break;
-    case EPI_UPDATE: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_UPDATE>), dim3(grid), dim3(256), 0, s, set, args); break;
-    case EPI_FFG: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_FFG>), dim3(grid), dim3(256), 0, s, set, args); break;
-    default: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN>), dim3(grid), dim3(256), 0, s, set, args); break;
+    case EPI_ERROR: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_ERROR>), dim3(grid), block, 0, s, set, args); break;
+    case EPI_UPDATE: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_UPDATE>), dim3(grid), block, 0, s, set, args); break;
+    case EPI_FFG: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_FFG>), dim3(grid), block, 0, s, set, args); break;
+    default: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN>), dim3(grid), block, 0, s, set, args); break;
     }
     return hipGetLastError();
 }

@@ -11,8 +11,8 @@
 
 namespace pcd {
 
-// Launches phase_kernel<OP, BM, BN, epi> over `grid` workgroups of 256 threads
-// on `stream` and returns the launch status.
+// Launches phase_kernel<OP, BM, BN, epi> over `grid` workgroups of
+// TileCfg<BM, BN>::NT threads on `stream` and returns the launch status.
 template <typename OP, int BM, int BN>
 hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t stream);
 

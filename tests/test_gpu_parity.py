@@ -197,3 +197,20 @@ def test_device_errors_are_status_codes():
             m.set_option("tile", 96)
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("path", __import__("tests.golden.make_golden", fromlist=["fixtures"]).fixtures(),
+                         ids=lambda p: p.rsplit("/", 1)[-1][:-4])
+def test_golden_fixtures_fp32(path):
+    # float64 autograd fixtures (tests/golden): the fp32 HIP path within 1e-4*(1+|x|)
+    from tests.golden.make_golden import load
+    from predicitivecoding_amd import GenerativeSnapshot
+    from tests.gpu_util import ACT_ID
+    g = load(path)
+    snap = GenerativeSnapshot(g["sizes"], ACT_ID[g["act"]], g["eta"], g["act_reg"], g["ffg"], g["W"], g["b"],
+                              list(g["precisions"]))
+    top, st, en = run_gpu(snap, g["x"], g["steps"], states=True, energy=True)
+    errs = dict(top=max_rel(top, g["top"]), energy=max_rel(en, g["energy"]),
+                states=max(max_rel(a, r) for a, r in zip(st, g["states"])))
+    _report(f"golden/{g['name']}", **errs)
+    assert all(v < 1e-4 for v in errs.values()), errs
