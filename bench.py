@@ -10,8 +10,10 @@ Workloads:
   c2  1024-1024-1024-1024-256 tanh fp32, B=1024, T=50, eta=0.05, x0~N(0,1)   (default)
   c3  6 x 4096 GELU bf16 operands, B=4096, T=32, eta=0.05, W~N(0,1/fan_in)
   c5  12 x 8192 GELU bf16 operands, B=8192, T=16, eta=0.02, W~N(0,1/fan_in)
-(c4, the ragged early-exit workload, is timed by --config c4 through the
-ragged entry point.)
+  c4  ragged: 64 requests on a shared 4 x 2048 tanh fp32 network, per-request
+      batch log-uniform in [1,512] and T uniform in [8,64] (seeded), early exit
+      when energy/sample < 1e-3; one pass = one packed pcd_pc_relax_ragged call,
+      value = sum over requests of rows x steps actually run / elapsed.
 
 The JSON line carries the roofline of the dominant kernel (average duration
 of its launches from HIP events on the library's stream) and a CPU baseline:
@@ -39,12 +41,27 @@ CONFIGS = {
                init="xavier"),
     "c3": dict(sizes=[4096] * 6, act=4, dtype="bf16", batch=4096, T=32, eta=0.05, x="normal", init="fanin"),
     "c5": dict(sizes=[8192] * 12, act=4, dtype="bf16", batch=8192, T=16, eta=0.02, x="normal", init="fanin"),
+    # eta and the initialisation are unstated for c4: NetworkConfig's default state rate (0.1) and
+    # Xavier-normal, the reference's tanh initialiser
+    "c4": dict(sizes=[2048] * 4, act=1, dtype="f32", eta=0.1, x="normal", init="xavier", requests=64,
+               bmax=512, tmin=8, tmax=64, exit_rule="absolute", exit_thr=1e-3, seed=4),
 }
 ACT_NAME = {1: "tanh", 4: "gelu"}
 
 
 def flops_per_sample_step(sizes):
     return 4.0 * sum(sizes[l] * sizes[l - 1] for l in range(1, len(sizes)))
+
+
+def make_ragged_requests(cfg):
+    """Per-request rows (log-uniform in [1, bmax]) and step budgets (uniform in
+    [tmin, tmax]) from the config's seed."""
+    rng = np.random.default_rng(cfg["seed"])
+    rows = np.floor(np.exp(rng.uniform(0.0, np.log(cfg["bmax"]), cfg["requests"]))).astype(np.int64)
+    rows = np.clip(rows, 1, cfg["bmax"]).astype(np.int32)
+    steps = rng.integers(cfg["tmin"], cfg["tmax"] + 1, cfg["requests"]).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)
+    return offsets, steps
 
 
 def make_weights(cfg, seed=0):
@@ -187,6 +204,114 @@ def traffic_from_pmc(workload, fetch_dir, write_dir, calib_fetch_dir, calib_writ
         json.dump(out, f, indent=1)
     print(json.dumps(out, indent=1))
 
+def bench_ragged(args, cfg):
+    """c4: one pass = one packed pcd_pc_relax_ragged call over every request."""
+    import torch
+    from predicitivecoding_amd import GenerativeSnapshot, PcDeviceModel
+    sizes = cfg["sizes"]
+    offsets, steps = make_ragged_requests(cfg)
+    rows, R = int(offsets[-1]), len(steps)
+    print(f"# bench c4: sizes={sizes} requests={R} rows={rows} steps {steps.min()}..{steps.max()} "
+          f"exit {cfg['exit_rule']} < {cfg['exit_thr']}", file=sys.stderr, flush=True)
+    W, b = make_weights(cfg)
+    snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
+    model = PcDeviceModel(snap, cfg["dtype"])
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn((rows, sizes[0]), generator=g, device="cuda", dtype=torch.float32)
+    top = torch.empty((rows, sizes[-1]), device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+
+    def one_pass():
+        return model.relax_ragged_device(x.data_ptr(), offsets, steps, top.data_ptr(), cfg["exit_rule"],
+                                         cfg["exit_thr"])
+
+    for _ in range(args.warmup):
+        one_pass()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    done = 0
+    for _ in range(args.steps):
+        used, _ = one_pass()
+        done += int(np.sum(np.diff(offsets).astype(np.int64) * used))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    value = done / elapsed
+    ms_per_step = elapsed * 1e3 / args.steps
+    print(f"# timed {args.steps} passes: {ms_per_step:.3f} ms/pass, {value:.4g} sample-steps/s, "
+          f"{int(np.sum(used < steps))} of {R} requests exited early", file=sys.stderr, flush=True)
+
+    # Per-launch timing of the phases (eager, HIP events on the library's
+    # stream) and the FLOPs those launches did: at step t the rows of every
+    # request still running.
+    model.set_option("profile", 1)
+    used, _ = one_pass()
+    err_ms, upd_ms, launches = model.profile_result()
+    model.set_option("profile", 0)
+    per_row = np.diff(offsets).astype(np.float64)
+    active = np.array([per_row[used > t].sum() for t in range(int(steps.max()))])
+    S = sum(sizes[l] * sizes[l - 1] for l in range(1, len(sizes)))
+    flop_launch = 2.0 * S * active.mean()             # mean over the launches of one phase
+    dom_name, dom_ms = ("update_phase", upd_ms) if upd_ms >= err_ms else ("error_phase", err_ms)
+    achieved = flop_launch / (dom_ms * 1e-3)
+    peak = PEAK[cfg["dtype"]]
+    roofline = {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / peak, "traffic": traffic_from_profiles("c4", dom_name), "kernel": dom_name,
+                "kernel_ms": dom_ms, "error_phase_ms": err_ms, "update_phase_ms": upd_ms, "launches_timed": launches,
+                "flop_per_launch": flop_launch, "mean_active_rows": float(active.mean()),
+                "path_frac": 4.0 * S * value / peak}
+    print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch over {launches} steps, "
+          f"{active.mean():.0f} active rows on average; {dom_name} at {achieved / 1e12:.1f} TFLOP/s = "
+          f"{100 * achieved / peak:.1f}% of peak", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_ragged(cfg, W, b, x.cpu().numpy(), offsets, steps, args.cpu_budget)
+        print(f"# cpu baseline: {cpu['value']:.4g} sample-steps/s on {cpu['cores']} threads", file=sys.stderr,
+              flush=True)
+    rec = {
+        "metric": "relaxed samples*steps/sec at 1 GPU and % of MFMA/HBM roofline",
+        "value": value, "unit": "sample-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": cfg["dtype"], "data": "synthetic (seeded random weights, inputs and request shapes)",
+        "config": {"workload": f"c4: ragged, {R} requests on {'-'.join(map(str, sizes))} tanh f32, rows log-uniform "
+                               f"[1,{cfg['bmax']}], T uniform [{cfg['tmin']},{cfg['tmax']}], exit E/rows < "
+                               f"{cfg['exit_thr']}, eta={cfg['eta']}",
+                   "requests": R, "rows": rows, "layer_sizes": sizes, "parallelism": "single GPU"},
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec))
+    model.close()
+
+
+def cpu_baseline_ragged(cfg, W, b, x_host, offsets, steps, budget_s=10.0):
+    """The oracle's per-request relaxation with the same exit rule, on the
+    first requests that fit the time budget."""
+    from oracle import pc_oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    pc_oracle.set_threads(threads)
+    sizes, P = cfg["sizes"], [1.0] * len(cfg["sizes"])
+    n = min(16, int(offsets[-1]))
+    pc_oracle.batched_relax(sizes, "tanh", cfg["eta"], W, b, P, x_host[:n], 1)
+    t0 = time.perf_counter()
+    pc_oracle.batched_relax(sizes, "tanh", cfg["eta"], W, b, P, x_host[:n], 2)
+    per = (time.perf_counter() - t0) / (2 * n)
+    rows = np.diff(offsets)
+    k, est = 0, 0.0
+    while k < len(steps) and est + rows[k] * steps[k] * per <= budget_s:
+        est += rows[k] * steps[k] * per
+        k += 1
+    k = max(k, 1)
+    sub_off = offsets[:k + 1]
+    t0 = time.perf_counter()
+    used, _, _ = pc_oracle.ragged_relax(sizes, "tanh", cfg["eta"], W, b, P, x_host[:int(sub_off[-1])], sub_off,
+                                        steps[:k], cfg["exit_rule"], cfg["exit_thr"])
+    dt = time.perf_counter() - t0
+    done = int(np.sum(rows[:k].astype(np.int64) * used))
+    return {"value": done / dt, "unit": "sample-steps/s", "cores": threads, "kind": "port",
+            "sample": f"oracle per-request fp32 relaxation with the same exit rule, first {k} of {len(steps)} "
+                      f"requests ({int(sub_off[-1])} rows, {done} sample-steps), {dt:.1f} s"}
+
+
 
 def main():
     ap = argparse.ArgumentParser()
@@ -220,6 +345,9 @@ def main():
     from predicitivecoding_amd import GenerativeSnapshot, PcDeviceModel
 
     cfg = CONFIGS[args.config]
+    if args.config == "c4":
+        bench_ragged(args, cfg)
+        return
     sizes, B, T = cfg["sizes"], cfg["batch"], cfg["T"]
     print(f"# bench {args.config}: sizes={sizes} B={B} T={T} dtype={cfg['dtype']}", file=sys.stderr, flush=True)
     W, b = make_weights(cfg)

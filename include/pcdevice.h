@@ -209,7 +209,8 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  * hooks for the host wrappers and the benchmark):
  *   use_graph    capture the T-step loop in a hipGraph (default 1)
  *   tile_m/n     force a GEMM tile (0 = automatic choice)
- *   profile      record per-kernel HIP events on the next eager run */
+ *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
+ *                time every phase launch with HIP events (pcd_pc_profile_result) */
 int pcd_pc_set_option(pcd_model* model, const char* name, int value);
 /* Average duration (ms) of the error-phase and update-phase kernels over the
  * launches of the last profiled call, and their launch counts. */

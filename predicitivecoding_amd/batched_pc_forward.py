@@ -104,6 +104,23 @@ class PcDeviceModel:
                     t.free()
         return top_h, states, energy
 
+    def relax_ragged_device(self, x0_ptr: int, row_offsets, steps, top_ptr: int, exit_rule: str = "none",
+                            exit_threshold: float = 0.0, stream: Stream | None = None):
+        """pcd_pc_relax_ragged on device input/output pointers (the call
+        synchronises its stream); returns (steps_used, final_energy)."""
+        offs = np.ascontiguousarray(row_offsets, dtype=np.int32)
+        st = np.ascontiguousarray(steps, dtype=np.int32)
+        R = len(st)
+        used = np.zeros(R, dtype=np.int32)
+        fe = np.zeros(R, dtype=np.float32)
+        if exit_rule not in EXIT:
+            raise ArgumentException(f"exit_rule must be one of {sorted(EXIT)}")
+        call("pcd_pc_relax_ragged", self.handle, x0_ptr,
+             offs.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), st.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+             R, EXIT[exit_rule], float(exit_threshold), used.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+             top_ptr, fe.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), stream.handle if stream else None)
+        return used, fe
+
     def relax_ragged(self, x0_packed: np.ndarray, row_offsets, steps, exit_rule: str = "none",
                      exit_threshold: float = 0.0, stream: Stream | None = None):
         """Ragged requests with early exit; returns (steps_used, final_energy, top)."""

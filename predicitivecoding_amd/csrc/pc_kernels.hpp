@@ -5,13 +5,16 @@
 //   error phase   for every layer l = 1..L-1 at once (independent problems):
 //                   PRE  = S_l . W_l^T           MFMA GEMM [B x s_{l-1}], K = s_l
 //                   pred = f(PRE + b_l)
-//                   e    = P_{l-1} (M_{l-1} - pred)         -> E_{l-1} (fp32)
+//                   e    = P_{l-1} (M_{l-1} - pred)
 //                   d    = f'(PRE + b_l) * e                -> D_l (operand type)
+//                   X    = M_{l-1} - eta (e + lambda sign(M_{l-1}))  -> X_{l-1} (fp32)
 //                   energy partial 0.5 e^2 / P_{l-1}, summed per row
 //   update phase  for every layer l = 1..L-1 at once:
 //                   G    = D_l . W_l                 MFMA GEMM [B x s_l], K = s_{l-1}
-//                   M_l -= eta (E_l - G + lambda sign(M_l))  (E_{L-1} = 0)
+//                   M_l  = X_l + eta G   (top layer, E = 0: M_l -= eta (lambda sign(M_l) - G))
 //                   S_l  = operand-type copy of M_l
+// which is the reference's M_l -= eta (E_l - G + lambda sign(M_l)) with the
+// terms known before the GEMM folded into X by the phase that has M_l at hand.
 //
 // Both GEMMs read their operands K-contiguous ("A . B^T" with A [rows x K] and
 // B [N x K] row-major): the error phase uses W_l as stored ([s_{l-1} x s_l]),
@@ -66,6 +69,18 @@ __device__ __forceinline__ void static_for(F&& f) {
 enum Act { ACT_LINEAR = 0, ACT_TANH = 1, ACT_RELU = 2, ACT_SIGMOID = 3, ACT_GELU = 4 };
 enum Epi { EPI_ERROR = 0, EPI_UPDATE = 1, EPI_FFG = 2, EPI_PLAIN = 3 };
 
+// Global-memory accessors.  The epilogue pointers arrive through the
+// kernel-argument struct as generic pointers; accessing them through the
+// global address space gives global_load/global_store instead of flat ones
+// (which also count against the LDS wait counter).
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) uint16_t gu16;
+typedef __attribute__((address_space(1))) int gint;
+__device__ __forceinline__ float gld(const float* p) { return *(const gfloat*)p; }
+__device__ __forceinline__ int gld(const int* p) { return *(const gint*)p; }
+__device__ __forceinline__ void gst(float* p, float v) { *(gfloat*)p = v; }
+__device__ __forceinline__ void gst(uint16_t* p, uint16_t v) { *(gu16*)p = v; }
+
 // bf16 and fp16 are carried as raw 16-bit patterns.
 struct bf16_t { uint16_t v; };
 struct f16_t { uint16_t v; };
@@ -80,11 +95,11 @@ struct Problem {
     int ldo;              // leading dimension of every [rows x N] epilogue operand
     const float* bias;    // ERROR/FFG: b_l [N]
     const float* mlow;    // ERROR: fp32 state M_{l-1}
-    float* eout;          // ERROR: E_{l-1} (nullable: layer 0 is never updated)
+    float* eout;          // ERROR: X_{l-1} = M - eta (E + lambda sign M) (nullable: layer 0 is never updated)
     void* dout;           // ERROR: D_l in the operand type; FFG: operand-type state copy
     float* m;             // UPDATE: fp32 state M_l (in/out); FFG: state out; PLAIN: C
     void* mop;            // UPDATE: operand-type copy of M_l (nullable for fp32)
-    const float* eself;   // UPDATE: E_l (nullable for the top layer)
+    const float* eself;   // UPDATE: X_l from the error phase (nullable for the top layer)
     float prec;           // ERROR: P_{l-1}
     int slot_base;        // ERROR: first energy partial slot of this problem
 };
@@ -186,15 +201,15 @@ __device__ __forceinline__ uint16_t to_f16(float x) {
 template <typename OP> struct OpTraits;
 template <> struct OpTraits<float> {
     static constexpr int bytes = 4;
-    __device__ static void store(void* base, size_t idx, float v) { ((float*)base)[idx] = v; }
+    __device__ static void store(void* base, size_t idx, float v) { gst((float*)base + idx, v); }
 };
 template <> struct OpTraits<bf16_t> {
     static constexpr int bytes = 2;
-    __device__ static void store(void* base, size_t idx, float v) { ((uint16_t*)base)[idx] = to_bf16(v); }
+    __device__ static void store(void* base, size_t idx, float v) { gst((uint16_t*)base + idx, to_bf16(v)); }
 };
 template <> struct OpTraits<f16_t> {
     static constexpr int bytes = 2;
-    __device__ static void store(void* base, size_t idx, float v) { ((uint16_t*)base)[idx] = to_f16(v); }
+    __device__ static void store(void* base, size_t idx, float v) { gst((uint16_t*)base + idx, to_f16(v)); }
 };
 
 // One 32-byte K chunk of a 32x32 block: a and b hold this lane's 16 bytes.
@@ -224,7 +239,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 
 // Row activity of the ragged path: the row's request still runs at step t.
 __device__ __forceinline__ bool row_active(const PhaseArgs& a, int row) {
-    return a.row_req == nullptr || a.t < a.done_at[a.row_req[row]];
+    return a.row_req == nullptr || a.t < gld(a.done_at + gld(a.row_req + row));
 }
 
 // LDS layout of one pipeline stage: rows of RB bytes (the K slice of one A or
@@ -300,8 +315,8 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     if (EPI == EPI_UPDATE && args.energy_out != nullptr) {
         for (int row = blockIdx.x * C::NT + tid; row < args.batch; row += gridDim.x * C::NT) {
             float s = 0.f;
-            for (int k = 0; k < args.nslots; ++k) s += args.energy_part[(size_t)k * args.ldp + row];
-            args.energy_out[(size_t)args.t * args.batch + row] = s;
+            for (int k = 0; k < args.nslots; ++k) s += gld(args.energy_part + (size_t)k * args.ldp + row);
+            gst(args.energy_out + (size_t)args.t * args.batch + row, s);
         }
     }
 
@@ -440,85 +455,115 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     auto row_of = [&](int i, int r) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
     auto col_of = [&](int j) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + lr; };
     if constexpr (EPI == EPI_ERROR) {
-        // Blocks b = i*FN + j in order; the M_{l-1} operands of the next PD
-        // blocks are in flight while a block computes, so the load latency is
-        // paid about once per tile instead of once per block.
-        constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
-        const float P_low = P.prec, inv2p = 0.5f / P.prec;
-        const bool want_energy = args.energy_part != nullptr;
-        float mv[PD][16];
-        float esum[16];
-        auto load_block = [&](auto Bc) PCD_INLINE {
-            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
-            const int col = col_of(j);
-            static_for<0, 16>([&](auto R) PCD_INLINE {
-                constexpr int r = decltype(R)::value;
-                const int row = row_of(i, r);
-                mv[b % PD][r] = (col < P.N && row < P.M) ? P.mlow[(size_t)row * P.ldo + col] : 0.f;
-            });
-        };
-        static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
-        static_for<0, NB>([&](auto Bc) PCD_INLINE {
-            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
-            if constexpr (j == 0) static_for<0, 16>([&](auto R) PCD_INLINE { esum[decltype(R)::value] = 0.f; });
-            const int col = col_of(j);
-            const bool cok = col < P.N;
-            const float bj = cok ? P.bias[col] : 0.f;
-            static_for<0, 16>([&](auto R) PCD_INLINE {
-                constexpr int r = decltype(R)::value;
-                const int row = row_of(i, r);
-                if (cok && row < P.M && row_active(args, row)) {
-                    const size_t idx = (size_t)row * P.ldo + col;
-                    const float pre = acc[i][j][r] + bj;
-                    float y, dy;
-                    act_eval(args.act, pre, y, dy);
-                    const float e = P_low * (mv[b % PD][r] - y);
-                    const float d = dy * e;
-                    OpTraits<OP>::store(P.dout, idx, d);
-                    if (P.eout) P.eout[idx] = e;
-                    esum[r] += e * e * inv2p;
-                }
-            });
-            if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
-            if constexpr (j == C::FN - 1) {
-                if (want_energy) {
-                    static_for<0, 16>([&](auto R) PCD_INLINE {
-                        constexpr int r = decltype(R)::value;
-                        float v = esum[r];
-                        v += __shfl_xor(v, 16);
-                        v += __shfl_xor(v, 8);
-                        v += __shfl_xor(v, 4);
-                        v += __shfl_xor(v, 2);
-                        v += __shfl_xor(v, 1);
-                        esum[r] = v;
-                    });
-                    if (lr == 0) {
-                        const int slot = P.slot_base + tn * C::WN + wn;
+        // On the 256 x 256 tile (the large 16-bit models), one copy of the
+        // epilogue per activation, chosen once per tile: the per-element
+        // activation switch would otherwise stay in the code (measured 15%
+        // of the epilogue).  Smaller tiles keep one generic copy, which
+        // compiles several times faster.
+        auto epilogue = [&](auto ActC) PCD_INLINE {
+            constexpr int ACT = decltype(ActC)::value;
+            // Blocks b = i*FN + j in order; the M_{l-1} operands of the next PD
+            // blocks are in flight while a block computes, so the load latency is
+            // paid about once per tile instead of once per block.
+            constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
+            const float P_low = P.prec, inv2p = 0.5f / P.prec;
+            const float eta = args.eta, lam = args.act_reg;
+            const bool want_energy = args.energy_part != nullptr;
+            float mv[PD][16];
+            float esum[16];
+            auto load_block = [&](auto Bc) PCD_INLINE {
+                constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+                const int col = col_of(j);
+                static_for<0, 16>([&](auto R) PCD_INLINE {
+                    constexpr int r = decltype(R)::value;
+                    const int row = row_of(i, r);
+                    mv[b % PD][r] = (col < P.N && row < P.M) ? gld(P.mlow + (size_t)row * P.ldo + col) : 0.f;
+                });
+            };
+            static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
+            static_for<0, NB>([&](auto Bc) PCD_INLINE {
+                constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+                if constexpr (j == 0) static_for<0, 16>([&](auto R) PCD_INLINE { esum[decltype(R)::value] = 0.f; });
+                const int col = col_of(j);
+                const bool cok = col < P.N;
+                const float bj = cok ? gld(P.bias + col) : 0.f;
+                static_for<0, 16>([&](auto R) PCD_INLINE {
+                    constexpr int r = decltype(R)::value;
+                    const int row = row_of(i, r);
+                    if (cok && row < P.M && row_active(args, row)) {
+                        const size_t idx = (size_t)row * P.ldo + col;
+                        const float pre = acc[i][j][r] + bj;
+                        float y, dy;
+                        act_eval(ACT >= 0 ? ACT : args.act, pre, y, dy);
+                        const float m = mv[b % PD][r];
+                        const float e = P_low * (m - y);
+                        const float d = dy * e;
+                        OpTraits<OP>::store(P.dout, idx, d);
+                        // The state's own part of its update, folded here while
+                        // M_{l-1} is in registers: X = M - eta (e + lambda sign M).
+                        // The update phase then only adds eta * (W^T D).
+                        if (P.eout) {
+                            float g = e;
+                            if (lam > 0.f) g += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
+                            gst(P.eout + idx, m - eta * g);
+                        }
+                        esum[r] += e * e * inv2p;
+                    }
+                });
+                if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
+                if constexpr (j == C::FN - 1) {
+                    if (want_energy) {
                         static_for<0, 16>([&](auto R) PCD_INLINE {
                             constexpr int r = decltype(R)::value;
-                            const int row = row_of(i, r);
-                            if (row < P.M) args.energy_part[(size_t)slot * args.ldp + row] = esum[r];
+                            float v = esum[r];
+                            v += __shfl_xor(v, 16);
+                            v += __shfl_xor(v, 8);
+                            v += __shfl_xor(v, 4);
+                            v += __shfl_xor(v, 2);
+                            v += __shfl_xor(v, 1);
+                            esum[r] = v;
                         });
+                        if (lr == 0) {
+                            const int slot = P.slot_base + tn * C::WN + wn;
+                            static_for<0, 16>([&](auto R) PCD_INLINE {
+                                constexpr int r = decltype(R)::value;
+                                const int row = row_of(i, r);
+                                if (row < P.M) gst(args.energy_part + (size_t)slot * args.ldp + row, esum[r]);
+                            });
+                        }
                     }
                 }
+                __builtin_amdgcn_sched_barrier(0);  // the next block starts after this one's loads are issued
+            });
+        };
+        if constexpr (C::BIG) {
+            switch (args.act) {
+            case ACT_TANH: epilogue(std::integral_constant<int, ACT_TANH>{}); break;
+            case ACT_RELU: epilogue(std::integral_constant<int, ACT_RELU>{}); break;
+            case ACT_SIGMOID: epilogue(std::integral_constant<int, ACT_SIGMOID>{}); break;
+            case ACT_GELU: epilogue(std::integral_constant<int, ACT_GELU>{}); break;
+            default: epilogue(std::integral_constant<int, ACT_LINEAR>{}); break;
             }
-            __builtin_amdgcn_sched_barrier(0);  // the next block starts after this one's loads are issued
-        });
+        } else {
+            epilogue(std::integral_constant<int, -1>{});   // activation chosen per element
+        }
     } else if constexpr (EPI == EPI_UPDATE) {
-        // As the error epilogue: M_l and E_l of the next PD blocks in flight.
-        constexpr int NB = C::FM * C::FN, PD = NB < 2 ? NB : 2;
+        // M_l = X_l + eta G for the layers below the top, X_l = M_l - eta (E_l +
+        // lambda sign M_l) having been written by the error phase; the top
+        // layer (E = 0) reads M_l itself: M_l -= eta (lambda sign M_l - G).
+        // The operand of the next PD blocks is in flight while a block computes.
+        constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
         const float eta = args.eta, lam = args.act_reg;
-        float mv[PD][16], ev[PD][16];
+        const bool folded = P.eself != nullptr;
+        const float* src = folded ? P.eself : P.m;
+        float xv[PD][16];
         auto load_block = [&](auto Bc) PCD_INLINE {
             constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
             const int col = col_of(j);
             static_for<0, 16>([&](auto R) PCD_INLINE {
                 constexpr int r = decltype(R)::value;
                 const int row = row_of(i, r);
-                const bool ok = col < P.N && row < P.M;
-                const size_t idx = (size_t)row * P.ldo + col;
-                mv[b % PD][r] = ok ? P.m[idx] : 0.f;
-                ev[b % PD][r] = ok && P.eself ? P.eself[idx] : 0.f;
+                xv[b % PD][r] = (col < P.N && row < P.M) ? gld(src + (size_t)row * P.ldo + col) : 0.f;
             });
         };
         static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
@@ -531,11 +576,16 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                     const int row = row_of(i, r);
                     if (row < P.M && row_active(args, row)) {
                         const size_t idx = (size_t)row * P.ldo + col;
-                        float m = mv[b % PD][r];
-                        float grad = ev[b % PD][r] - acc[i][j][r];
-                        if (lam > 0.f) grad += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
-                        m -= eta * grad;
-                        P.m[idx] = m;
+                        const float x = xv[b % PD][r];
+                        float m;
+                        if (folded) {
+                            m = x + eta * acc[i][j][r];
+                        } else {
+                            float grad = -acc[i][j][r];
+                            if (lam > 0.f) grad += lam * (x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f));
+                            m = x - eta * grad;
+                        }
+                        gst(P.m + idx, m);
                         if (P.mop) OpTraits<OP>::store(P.mop, idx, m);
                     }
                 });
@@ -551,14 +601,14 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                 __builtin_amdgcn_sched_barrier(0);  // keep each block's epilogue to itself
                 const int col = col_of(j);
                 if (col < P.N) {
-                    const float bj = P.bias[col];
+                    const float bj = gld(P.bias + col);
                     static_for<0, 16>([&](auto R) PCD_INLINE {
                         constexpr int r = decltype(R)::value;
                         const int row = row_of(i, r);
                         if (row < P.M) {
                             const size_t idx = (size_t)row * P.ldo + col;
                             const float y = act_f(args.act, acc[i][j][r] + bj);
-                            P.m[idx] = y;
+                            gst(P.m + idx, y);
                             if (P.dout) OpTraits<OP>::store(P.dout, idx, y);
                         }
                     });
@@ -579,8 +629,8 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                         if (row < P.M) {
                             const size_t idx = (size_t)row * P.ldo + col;
                             float v = args.alpha * acc[i][j][r];
-                            if (args.beta != 0.f) v += args.beta * P.m[idx];
-                            P.m[idx] = v;
+                            if (args.beta != 0.f) v += args.beta * gld(P.m + idx);
+                            gst(P.m + idx, v);
                         }
                     });
                 }

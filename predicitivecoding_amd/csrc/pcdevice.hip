@@ -205,7 +205,7 @@ struct Workspace {
     std::vector<float*> M;             // [L] fp32 states (M[0] = clamped input)
     std::vector<void*> S;              // [L] operand-type state copies (16-bit dtypes only)
     std::vector<void*> D;              // [L] D_l, l >= 1, operand type [cap x P_{l-1}]
-    std::vector<float*> E;             // [L] E_l, 1 <= l <= L-2, fp32 [cap x P_l]
+    std::vector<float*> E;             // [L] X_l = M_l - eta (E_l + lambda sign M_l), 1 <= l <= L-2, fp32 [cap x P_l]
     float* energy_part = nullptr;      // [slots x cap]
     int slots_cap = 0;
     hipStream_t capture = nullptr;     // private stream used for graph capture
@@ -424,6 +424,30 @@ PhaseArgs base_args(const pcd_model* m, const Workspace* w, int batch, int nslot
 struct PhaseTimer {
     std::vector<std::pair<hipEvent_t, hipEvent_t>> err, upd;
 };
+
+// Waits for the timed launches, stores the average error- and update-phase
+// durations in the model, and destroys the events (also after a failure).
+int collect_timer(pcd_model* m, PhaseTimer& timer, hipStream_t s) {
+    hipError_t e = hipStreamSynchronize(s);
+    double te = 0, tu = 0;
+    for (size_t i = 0; i < timer.upd.size() && e == hipSuccess; ++i) {
+        float a = 0, b = 0;
+        e = hipEventElapsedTime(&a, timer.err[i].first, timer.err[i].second);
+        if (e == hipSuccess) e = hipEventElapsedTime(&b, timer.upd[i].first, timer.upd[i].second);
+        te += a;
+        tu += b;
+    }
+    for (auto& p : timer.err) {
+        (void)hipEventDestroy(p.first);
+        (void)hipEventDestroy(p.second);
+    }
+    for (auto& p : timer.upd) (void)hipEventDestroy(p.second);  // its first event is the error phase's second
+    if (e != hipSuccess) return from_hip(e, "phase timing");
+    m->prof_launches = (int)timer.upd.size();
+    m->prof_err_ms = m->prof_launches ? (float)(te / m->prof_launches) : 0.f;
+    m->prof_upd_ms = m->prof_launches ? (float)(tu / m->prof_launches) : 0.f;
+    return PCD_SUCCESS;
+}
 
 int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, Tile tile, float* energy_out,
                   const int* row_req, int* done_at, const int* row_offsets_dev, int requests, int exit_rule,
@@ -994,24 +1018,9 @@ int pcd_pc_relax(pcd_model* m, const float* x0, int batch, int steps, float* out
         PhaseTimer timer;
         int st = enqueue_relax(m, w, batch, steps, tile, out_energy, nullptr, nullptr, nullptr, 0, 0, 0.f, nullptr,
                                nullptr, s, &timer);
+        int st2 = collect_timer(m, timer, s);
         if (st) return st;
-        HIP_TRY(hipStreamSynchronize(s));
-        double te = 0, tu = 0;
-        for (size_t i = 0; i < timer.err.size(); ++i) {
-            float a = 0, b2 = 0;
-            HIP_TRY(hipEventElapsedTime(&a, timer.err[i].first, timer.err[i].second));
-            HIP_TRY(hipEventElapsedTime(&b2, timer.upd[i].first, timer.upd[i].second));
-            te += a;
-            tu += b2;
-        }
-        for (size_t i = 0; i < timer.err.size(); ++i) {
-            (void)hipEventDestroy(timer.err[i].first);
-            (void)hipEventDestroy(timer.err[i].second);
-            (void)hipEventDestroy(timer.upd[i].second);
-        }
-        m->prof_launches = (int)timer.err.size();
-        m->prof_err_ms = m->prof_launches ? (float)(te / m->prof_launches) : 0.f;
-        m->prof_upd_ms = m->prof_launches ? (float)(tu / m->prof_launches) : 0.f;
+        if (st2) return st2;
     } else if (m->use_graph) {
         int st = PCD_SUCCESS;
         Plan* p = get_plan(m, w, batch, steps, out_energy != nullptr, tile, &st);
@@ -1082,9 +1091,17 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
         e = hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0_packed, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, rows,
                              hipMemcpyDeviceToDevice, s);
     if (e != hipSuccess) st = from_hip(e, "ragged upload");
-    if (!st)
+    if (!st) {
+        // With the profile option, every phase launch is timed (the ragged
+        // loop always runs eagerly).
+        PhaseTimer timer;
         st = enqueue_relax(m, w, rows, tmax, tile, nullptr, d_row_req, d_done, d_offsets, requests, exit_rule,
-                           exit_threshold, d_prev, d_last, s, nullptr);
+                           exit_threshold, d_prev, d_last, s, m->profile ? &timer : nullptr);
+        if (m->profile) {
+            int st2 = collect_timer(m, timer, s);
+            if (!st) st = st2;
+        }
+    }
     if (!st) st = copy_out_rows(out_top, m->s[L - 1], w->M[L - 1], m->P[L - 1], rows, s);
     std::vector<float> last(requests);
     if (!st) {

@@ -214,3 +214,34 @@ def test_golden_fixtures_fp32(path):
                 states=max(max_rel(a, r) for a, r in zip(st, g["states"])))
     _report(f"golden/{g['name']}", **errs)
     assert all(v < 1e-4 for v in errs.values()), errs
+
+
+@pytest.mark.parametrize("rule,thr", [("absolute", 1e-3), ("relative", 1e-2)])
+def test_c4_ragged_full_network(oracle, rule, thr):
+    # 64 ragged requests on a shared 4 x 2048 tanh fp32 network, rows log-uniform in
+    # [1,512], T uniform in [8,64], packed into one call.  Requests are independent, so each one's exit step,
+    # energy and top states must equal the oracle settling that request alone; the cheapest requests are checked.
+    import bench
+    from predicitivecoding_amd import PcDeviceModel
+    cfg = bench.CONFIGS["c4"]
+    offsets, steps = bench.make_ragged_requests(cfg)
+    sizes = cfg["sizes"]
+    snap, W, b, P, _ = build_case(sizes, "tanh", cfg["eta"], seed=21)
+    x = np.random.default_rng(22).standard_normal((int(offsets[-1]), sizes[0])).astype(np.float32)
+    if rule == "relative":
+        x *= np.float32(0.05)
+    m = PcDeviceModel(snap, "f32")
+    try:
+        used, fe, top = m.relax_ragged(x, offsets, steps, rule, thr)
+    finally:
+        m.close()
+    assert np.all(used >= 1) and np.all(used <= steps)
+    rows = np.diff(offsets)
+    for r in np.argsort(rows * steps)[:4]:
+        lo, hi = int(offsets[r]), int(offsets[r + 1])
+        rused, rfe, rtop = oracle.ragged_relax(sizes, "tanh", cfg["eta"], W, b, P, x[lo:hi], [0, hi - lo],
+                                               [int(steps[r])], rule, thr)
+        errs = dict(top=max_rel(top[lo:hi], rtop), energy=max_rel(fe[r:r + 1], rfe))
+        _report(f"c4/{rule}/request{r} rows={hi - lo} steps={steps[r]} used={used[r]}", **errs)
+        assert used[r] == rused[0], (r, used[r], rused[0])
+        assert all(v < 1e-4 for v in errs.values()), errs
