@@ -216,6 +216,8 @@ def bench_ragged(args, cfg):
     W, b = make_weights(cfg)
     snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
     model = PcDeviceModel(snap, cfg["dtype"])
+    if args.tile_order >= 0:
+        model.set_option("tile_order", args.tile_order)
     g = torch.Generator(device="cuda").manual_seed(1)
     x = torch.randn((rows, sizes[0]), generator=g, device="cuda", dtype=torch.float32)
     top = torch.empty((rows, sizes[-1]), device="cuda", dtype=torch.float32)
@@ -324,6 +326,7 @@ def main():
                     help="seconds the CPU baseline sample is sized for (its calibration overestimates ~2x)")
     ap.add_argument("--tile", type=int, default=0, help="force the GEMM tile rows (and columns unless --tile-n)")
     ap.add_argument("--tile-n", type=int, default=0)
+    ap.add_argument("--tile-order", type=int, default=-1, help="force the tile order option (0 interleaved, 1 contiguous)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the copy kernel that calibrates FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "CALIB_FETCH_DIR", "CALIB_WRITE_DIR"),
@@ -354,6 +357,8 @@ def main():
     W, b = make_weights(cfg)
     snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
     model = PcDeviceModel(snap, cfg["dtype"])
+    if args.tile_order >= 0:
+        model.set_option("tile_order", args.tile_order)
     if args.tile:
         model.set_option("tile", args.tile)
         if args.tile_n:

@@ -208,7 +208,9 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
 /* Relaxation options (no counterpart in the reference; tuning and profiling
  * hooks for the host wrappers and the benchmark):
  *   use_graph    capture the T-step loop in a hipGraph (default 1)
- *   tile_m/n     force a GEMM tile (0 = automatic choice)
+ *   tile, tile_n force a GEMM tile (0 = automatic choice)
+ *   tile_order   0: every XCD runs an eighth of each problem's tiles (default);
+ *                1: every XCD runs one contiguous eighth of the phase's tiles
  *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
  *                time every phase launch with HIP events (pcd_pc_profile_result) */
 int pcd_pc_set_option(pcd_model* model, const char* name, int value);

@@ -16,13 +16,15 @@ __global__ void zero_kernel(u32x4* __restrict__ p, size_t n) {
 }
 
 // Pack a row-major [rows x cols] fp32 matrix (optionally read transposed) into
-// a zero-padded [prow x pcol] buffer of the operand type.
+// a zero-padded [prow x pcol] buffer of the operand type whose rows are `ldd`
+// elements apart (ldd >= pcol; the columns past pcol are left alone).
 template <typename OP>
 __global__ void pack_kernel(const void* __restrict__ src, int src_is_f32, int rows, int cols, int trans,
-                            void* __restrict__ dst, int prow, int pcol) {
+                            void* __restrict__ dst, int prow, int pcol, int ldd) {
     size_t n = (size_t)prow * pcol;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        int r = (int)(i / pcol), c = (int)(i % pcol);
+    for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < n; k += (size_t)gridDim.x * blockDim.x) {
+        int r = (int)(k / pcol), c = (int)(k % pcol);
+        const size_t i = (size_t)r * ldd + c;
         float v = 0.f;
         bool inside = r < rows && c < cols;
         if (inside) {

@@ -91,7 +91,7 @@ struct Problem {
     const void* B;        // [>= tiles_n*BN rows x ldb], K-contiguous
     int lda, ldb;         // leading dimensions, elements
     int M, N, K;          // valid rows, valid columns, K (a multiple of the stage depth)
-    int tiles_m, tiles_n, tile_start;
+    int tiles_m, tiles_n, tiles;   // tile grid of the output, tiles = tiles_m * tiles_n
     int ldo;              // leading dimension of every [rows x N] epilogue operand
     const float* bias;    // ERROR/FFG: b_l [N]
     const float* mlow;    // ERROR: fp32 state M_{l-1}
@@ -134,7 +134,11 @@ struct PhaseArgs {
     int batch, t;
     const int* row_req;         // ragged: request of each row (nullable)
     const int* done_at;         // ragged: first step a request no longer runs
+    int tile_order;             // TILE_INTERLEAVED or TILE_CONTIGUOUS (see phase_grid)
 };
+
+// How a phase's tiles are dealt over the XCDs.
+enum TileOrder { TILE_INTERLEAVED = 0, TILE_CONTIGUOUS = 1 };
 
 // ------------------------------------------------------------ scalar helpers
 
@@ -212,14 +216,10 @@ template <> struct OpTraits<f16_t> {
     __device__ static void store(void* base, size_t idx, float v) { gst((uint16_t*)base + idx, to_f16(v)); }
 };
 
-// One 32-byte K chunk of a 32x32 block: a and b hold this lane's 16 bytes.
+// One 32-byte K chunk of a 32x32 block with 16-bit operands: a and b hold
+// this lane's 16 bytes (fp32 operands are issued per K component in the main
+// loop itself).
 template <typename OP> __device__ __forceinline__ void mfma_chunk(f32x16& acc, const u32x4& a, const u32x4& b);
-template <> __device__ __forceinline__ void mfma_chunk<float>(f32x16& acc, const u32x4& a, const u32x4& b) {
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[0]), __uint_as_float(b[0]), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[1]), __uint_as_float(b[1]), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[2]), __uint_as_float(b[2]), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[3]), __uint_as_float(b[3]), acc, 0, 0, 0);
-}
 template <> __device__ __forceinline__ void mfma_chunk<bf16_t>(f32x16& acc, const u32x4& a, const u32x4& b) {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
 }
@@ -227,14 +227,15 @@ template <> __device__ __forceinline__ void mfma_chunk<f16_t>(f32x16& acc, const
     acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
 }
 
-// Workgroup ids are dealt round-robin over the 8 XCDs; renumber them so that
-// consecutive logical tiles (which share operand rows) run on one XCD and
-// share its L2.
-__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
-    const int X = 8;
-    int q = nblocks / X, r = nblocks % X;
-    int x = bid % X, i = bid / X;
-    return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+// Workgroup ids are dealt round-robin over the XCDs (each with its own L2):
+// XCD x runs blocks x, x + 8, x + 16, ...
+constexpr int kXcds = 8;
+
+// Share of a problem's n tiles that XCD x runs: [lo, lo + cnt).  The shares
+// of the 8 XCDs tile [0, n) exactly and differ in size by at most one.
+__host__ __device__ __forceinline__ void xcd_share(int n, int x, int& lo, int& cnt) {
+    lo = n * x / kXcds;
+    cnt = n * (x + 1) / kXcds - lo;
 }
 
 // Row activity of the ragged path: the row's request still runs at step t.
@@ -254,6 +255,21 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
     return unit ^ ((row / (256 / RB)) % (RB / 16));
 }
 
+#ifndef PCD_BIG_RB
+#define PCD_BIG_RB 128
+#endif
+#ifndef PCD_BIG_NS
+#define PCD_BIG_NS 2
+#endif
+#ifndef PCD_MID_RB
+#define PCD_MID_RB 64
+#endif
+#ifndef PCD_MID_NS
+#define PCD_MID_NS 4
+#endif
+#ifndef PCD_OCC_SMALL
+#define PCD_OCC_SMALL 2
+#endif
 template <int BM, int BN> struct TileCfg {
     // 256 x 256 runs 8 waves (2 x 4 of 128 x 64: two waves per SIMD share the
     // MFMA pipe) over 128-byte K stages, double buffered (128 KB of LDS, one
@@ -264,19 +280,21 @@ template <int BM, int BN> struct TileCfg {
     static constexpr int NWAVES = WM * WN, NT = 64 * NWAVES;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
-    static constexpr int RB = BIG ? 128 : 64;              // K bytes per row per stage
+    static constexpr bool MID = BM == 128 && BN == 128;
+    static constexpr int RB = BIG ? PCD_BIG_RB : MID ? PCD_MID_RB : 64;       // K bytes per row per stage
     static constexpr int UNITS = RB / 16;                  // 16-byte units per row
     static constexpr int NC = RB / 32;                     // 32-byte MFMA chunks per stage
     static constexpr int stage_bytes = (BM + BN) * RB;
-    static constexpr int NS = BIG ? 2 : (BM == 256 && BN == 128) ? 3 : 4;   // stages in the LDS ring
+    static constexpr int NS = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : (BM == 256 && BN == 128) ? 3 : 4;   // stages in the LDS ring
     static constexpr int D = NS - 1;                       // prefetch distance (stages)
-    static constexpr int OCC = BIG ? 1 : 2;                // workgroups per CU the registers are sized for
+    static constexpr int OCC = BIG ? 1 : PCD_OCC_SMALL;    // workgroups per CU the registers are sized for
     static constexpr int ROWS_PER_LOAD = 64 * 16 / RB;     // rows one wave-wide 16-byte-per-lane load fills
     static constexpr int QPW = (BM + BN) / ROWS_PER_LOAD / NWAVES;   // loads per wave per stage
     static_assert(FM >= 1 && FN >= 1 && QPW >= 1, "tile too small");
     static_assert((BM + BN) % (NWAVES * ROWS_PER_LOAD) == 0, "stage rows must split evenly over the waves");
     static_assert(NC % 2 == 0, "fragment buffers alternate within a stage");
-    static_assert(D >= 1 && D <= 3, "stage_ready handles prefetch distances 1 to 3");
+    static_assert(D >= 1 && D <= 4, "stage_ready handles prefetch distances 1 to 4");
+    static_assert(NS * stage_bytes <= 160 * 1024, "LDS ring exceeds the 160 KB of a CU");
 };
 
 // Energy partial slots one tile column owns (one per wave column).
@@ -320,16 +338,49 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
         }
     }
 
-    const int bid = xcd_remap(blockIdx.x, gridDim.x);
     // `set` is the first kernel argument, so it sits at offset 0 of the kernarg
     // segment: index the problems there (scalar loads from constant memory)
     // instead of letting the compiler copy the whole set to scratch.
     typedef const __attribute__((address_space(4))) Problem KProblem;
     KProblem* kprobs = (KProblem*)__builtin_amdgcn_kernarg_segment_ptr();
-    int p = 0;
-    while (p + 1 < set.n && bid >= kprobs[p + 1].tile_start) ++p;
+    // XCD x runs the x-th eighth of every problem's tiles, problem after
+    // problem.  Every XCD, and every CU of it (an XCD deals its workgroups
+    // round-robin over its CUs), then gets a like share of the long-K and the
+    // short-K problems of a phase, and an eighth of one problem is a compact
+    // block of tiles that share operand rows in the XCD's L2.
+    // TILE_CONTIGUOUS instead gives XCD x one contiguous eighth of the phase's
+    // tiles taken in problem order (phases of many tiles per CU, where the
+    // balance evens out by itself).
+    const int x = blockIdx.x % kXcds;
+    int i = blockIdx.x / kXcds, p = 0, local = -1;
+    if (args.tile_order == TILE_INTERLEAVED) {
+        for (; p < set.n; ++p) {
+            int lo, cnt;
+            xcd_share(kprobs[p].tiles, x, lo, cnt);
+            if (i < cnt) {
+                local = lo + i;
+                break;
+            }
+            i -= cnt;
+        }
+    } else {
+        int total = 0;
+        for (int q = 0; q < set.n; ++q) total += kprobs[q].tiles;
+        int lo, cnt;
+        xcd_share(total, x, lo, cnt);
+        if (i < cnt) {
+            int t = lo + i;
+            for (; p < set.n; ++p) {
+                if (t < kprobs[p].tiles) {
+                    local = t;
+                    break;
+                }
+                t -= kprobs[p].tiles;
+            }
+        }
+    }
+    if (local < 0) return;  // a spare workgroup of this XCD (the grid is 8 x the largest XCD share)
     const Problem P = load_problem(kprobs + p);
-    int local = bid - P.tile_start;
     // Grouped order: runs of 8 row tiles share one column tile.
     const int G = 8;
     int group = local / (G * P.tiles_n);
@@ -341,17 +392,34 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     const int row0 = tm * BM, col0 = tn * BN;
 
     if (args.row_req != nullptr) {
-        bool act = false;
-        if (tid < BM) { int r = row0 + tid; act = r < P.M && row_active(args, r); }
-        if (!__syncthreads_or(act)) return;
+        // Any active row in the tile?  The flag borrows the first word of the
+        // (not yet used) stage ring, which the full ring leaves no room beside.
+        volatile int* flag = (volatile int*)smem;
+        if (tid == 0) *flag = 0;
+        __syncthreads();
+        if (tid < BM) {
+            const int r = row0 + tid;
+            if (r < P.M && row_active(args, r)) *flag = 1;
+        }
+        __syncthreads();
+        const bool any = *flag != 0;
+        __syncthreads();
+        if (!any) return;
     }
 
     // ---- main loop
-    f32x16 acc[C::FM][C::FN];
+    // fp32 MFMAs take K = 2 each, four per 32-byte chunk: with fewer than four
+    // output blocks per wave they rotate over NSPLIT accumulator sets (summed
+    // after the loop), so consecutive MFMAs never wait on each other's result.
+    constexpr bool F32OP = std::is_same<OP, float>::value;
+    constexpr int NSPLIT = (F32OP && C::FM * C::FN < 4) ? 4 / (C::FM * C::FN) : 1;
+    f32x16 accs[NSPLIT][C::FM][C::FN];
 #pragma unroll
-    for (int i = 0; i < C::FM; ++i)
+    for (int k = 0; k < NSPLIT; ++k)
 #pragma unroll
-        for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x16{};
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) accs[k][i][j] = f32x16{};
 
     const char* Ag = (const char*)P.A + (size_t)row0 * P.lda * OPB;
     const char* Bg = (const char*)P.B + (size_t)col0 * P.ldb * OPB;
@@ -393,17 +461,37 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
         }
     };
     auto mfmas = [&](const u32x4* a, const u32x4* b) PCD_INLINE {
-        static_for<0, C::FM>([&](auto I) PCD_INLINE {
-            static_for<0, C::FN>([&](auto J) PCD_INLINE {
-                mfma_chunk<OP>(acc[decltype(I)::value][decltype(J)::value], a[decltype(I)::value], b[decltype(J)::value]);
+        if constexpr (F32OP) {
+            // K component s of every block before component s + 1 of any.
+            static_for<0, 4>([&](auto Sc) PCD_INLINE {
+                constexpr int s = decltype(Sc)::value, k = s % NSPLIT;
+                static_for<0, C::FM>([&](auto I) PCD_INLINE {
+                    static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                        constexpr int i = decltype(I)::value, j = decltype(J)::value;
+                        accs[k][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[i][s]), __uint_as_float(b[j][s]),
+                                                                            accs[k][i][j], 0, 0, 0);
+                    });
+                });
             });
-        });
+        } else {
+            static_for<0, C::FM>([&](auto I) PCD_INLINE {
+                static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                    mfma_chunk<OP>(accs[0][decltype(I)::value][decltype(J)::value], a[decltype(I)::value],
+                                   b[decltype(J)::value]);
+                });
+            });
+        }
     };
     // Wait until stage `next` has landed for this wave, given how many later
     // stages are still in flight, then make it visible to all waves.
     auto stage_ready = [&](int next) PCD_INLINE {
         const int later = min(C::D - 1, nk - 1 - next);
-        if constexpr (C::D >= 3) {
+        if constexpr (C::D >= 4) {
+            if (later >= 3) wait_vmcnt<3 * C::QPW>();
+            else if (later == 2) wait_vmcnt<2 * C::QPW>();
+            else if (later == 1) wait_vmcnt<C::QPW>();
+            else wait_vmcnt<0>();
+        } else if constexpr (C::D >= 3) {
             if (later >= 2) wait_vmcnt<2 * C::QPW>();
             else if (later == 1) wait_vmcnt<C::QPW>();
             else wait_vmcnt<0>();
@@ -417,12 +505,16 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     };
     constexpr int NC = C::NC;
     u32x4 fa[2][C::FM], fb[2][C::FN];
+    // One LDS fragment read after each of the chunk's first MFMAs, the rest of
+    // the MFMAs after them.
+    constexpr int NMF = C::FM * C::FN * (F32OP ? 4 : 1);   // MFMAs per chunk
+    constexpr int NRD = C::FM + C::FN;                     // fragment reads per chunk
     auto interleave = [&]() PCD_INLINE {
-        static_for<0, C::FM + C::FN>([&](auto) PCD_INLINE {
+        static_for<0, NRD>([&](auto) PCD_INLINE {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         });
-        __builtin_amdgcn_sched_group_barrier(0x008, C::FM * C::FN - (C::FM + C::FN), 0);
+        if constexpr (NMF > NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
     };
     for (int s2 = 0; s2 < C::D && s2 < nk; ++s2) issue_stage(s2);
     stage_ready(0);
@@ -449,6 +541,13 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
         if constexpr (c + 1 < NC) read_frags((nk - 1) % C::NS, c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
         mfmas(fa[c & 1], fb[c & 1]);
     });
+    static_for<1, NSPLIT>([&](auto Kc) PCD_INLINE {
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) accs[0][i][j] += accs[decltype(Kc)::value][i][j];
+    });
+    f32x16 (&acc)[C::FM][C::FN] = accs[0];
 
     // ---- epilogue
     // Row of register r of a block in row-block i: 8*(r/4) + 4*half + r%4.

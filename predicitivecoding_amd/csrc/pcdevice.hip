@@ -169,9 +169,29 @@ int launch_op(Tile tile, int epi, const ProblemSet& set, const PhaseArgs& args, 
     return fail(PCD_INVALID_VALUE, "unsupported tile %d x %d", tile.m, tile.n);
 }
 
+// Workgroups of a phase launch: 8 x the most tiles any XCD runs (the kernel
+// deals the tiles over the XCDs with xcd_share, per problem or in one run).
+int phase_grid(const ProblemSet& set, int order) {
+    int most = 0, total = 0;
+    for (int i = 0; i < set.n; ++i) total += set.p[i].tiles;
+    for (int x = 0; x < kXcds; ++x) {
+        int sum = 0, lo, cnt;
+        if (order == TILE_INTERLEAVED) {
+            for (int i = 0; i < set.n; ++i) {
+                xcd_share(set.p[i].tiles, x, lo, cnt);
+                sum += cnt;
+            }
+        } else {
+            xcd_share(total, x, lo, cnt);
+            sum = cnt;
+        }
+        most = std::max(most, sum);
+    }
+    return most * kXcds;
+}
+
 int launch_phase(int dtype, Tile tile, int epi, const ProblemSet& set, const PhaseArgs& args, hipStream_t s) {
-    int grid = 0;
-    for (int i = 0; i < set.n; ++i) grid += set.p[i].tiles_m * set.p[i].tiles_n;
+    const int grid = phase_grid(set, args.tile_order);
     if (grid == 0) return PCD_SUCCESS;
     switch (dtype) {
     case PCD_F32: return launch_op<float>(tile, epi, set, args, grid, s);
@@ -228,7 +248,7 @@ struct pcd_model {
     int device = 0;
     int cus = 256;                      // compute units of the device
     int L = 0;
-    std::vector<int> s, P;              // sizes, padded sizes
+    std::vector<int> s, P;              // sizes, padded sizes (the GEMMs' K and every buffer's row pitch)
     int act = 0, ffg = 0, dtype = 0;
     float eta = 0.f, act_reg = 0.f;
     std::vector<float> prec;
@@ -237,7 +257,7 @@ struct pcd_model {
     std::mutex mu;
     std::vector<std::unique_ptr<Workspace>> ws;
     // options
-    int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0;
+    int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED;
     float prof_err_ms = 0.f, prof_upd_ms = 0.f;
     int prof_launches = 0;
     uint64_t clock = 0;
@@ -372,7 +392,6 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
     for (int l = L - 1; l >= 1; --l) {   // error phase: widest K first is irrelevant; keep layer order
         if (err.empty() || err.back().n == kMaxProblems) { err.emplace_back(); err.back().n = 0; }
         ProblemSet& ps = err.back();
-        int start = ps.n ? ps.p[ps.n - 1].tile_start + ps.p[ps.n - 1].tiles_m * ps.p[ps.n - 1].tiles_n : 0;
         Problem& p = ps.p[ps.n++];
         std::memset(&p, 0, sizeof p);
         p.A = state_operand(m, w, l);
@@ -384,7 +403,7 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         p.K = m->P[l];
         p.tiles_m = tm;
         p.tiles_n = (p.N + tile.n - 1) / tile.n;
-        p.tile_start = start;
+        p.tiles = p.tiles_m * p.tiles_n;
         p.ldo = m->P[l - 1];
         p.bias = m->bias[l];
         p.mlow = w->M[l - 1];
@@ -397,7 +416,6 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
     for (int l = 1; l < L; ++l) {
         if (upd.empty() || upd.back().n == kMaxProblems) { upd.emplace_back(); upd.back().n = 0; }
         ProblemSet& ps = upd.back();
-        int start = ps.n ? ps.p[ps.n - 1].tile_start + ps.p[ps.n - 1].tiles_m * ps.p[ps.n - 1].tiles_n : 0;
         Problem& p = ps.p[ps.n++];
         std::memset(&p, 0, sizeof p);
         p.A = w->D[l];
@@ -409,7 +427,7 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         p.K = m->P[l - 1];
         p.tiles_m = tm;
         p.tiles_n = (p.N + tile.n - 1) / tile.n;
-        p.tile_start = start;
+        p.tiles = p.tiles_m * p.tiles_n;
         p.ldo = m->P[l];
         p.m = w->M[l];
         p.mop = m->dtype == PCD_F32 ? nullptr : w->S[l];
@@ -430,6 +448,7 @@ PhaseArgs base_args(const pcd_model* m, const Workspace* w, int batch, int nslot
     a.ldp = w->cap;
     a.nslots = nslots;
     a.batch = batch;
+    a.tile_order = m->tile_order;
     return a;
 }
 
@@ -496,6 +515,7 @@ int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, Tile tile, f
             p.K = m->P[l];
             p.tiles_m = (batch + tile.m - 1) / tile.m;
             p.tiles_n = (p.N + tile.n - 1) / tile.n;
+            p.tiles = p.tiles_m * p.tiles_n;
             p.ldo = m->P[l - 1];
             p.bias = m->bias[l];
             p.m = w->M[l - 1];
@@ -804,9 +824,9 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     auto pack = [&](const void* src, int rows, int cols, int trans, void* dst, int prow, int pcol) -> int {
         int grid = (int)std::min<size_t>(((size_t)prow * pcol + 255) / 256, 8192);
         switch (dtype) {
-        case PCD_F32: hipLaunchKernelGGL(pack_kernel<float>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol); break;
-        case PCD_BF16: hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol); break;
-        default: hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol); break;
+        case PCD_F32: hipLaunchKernelGGL(pack_kernel<float>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
+        case PCD_BF16: hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
+        default: hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
         }
         return from_hip(hipGetLastError(), "pack_kernel launch");
     };
@@ -831,6 +851,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     p.K = kp;
     p.tiles_m = mp / tile.m;
     p.tiles_n = np / tile.n;
+    p.tiles = p.tiles_m * p.tiles_n;
     p.ldo = n;
     p.m = dC;
     PhaseArgs a;
@@ -923,16 +944,16 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
         int grid2 = (int)std::min<size_t>(((size_t)Rsz * m->P[l - 1] + 255) / 256, 8192);
         switch (dtype) {
         case PCD_F32:
-            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l]);
-            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1]);
+            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
+            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
             break;
         case PCD_BF16:
-            hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l]);
-            hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1]);
+            hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
+            hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
             break;
         default:
-            hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l]);
-            hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1]);
+            hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
+            hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
             break;
         }
         e = hipGetLastError();
@@ -985,7 +1006,11 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
             return fail(PCD_INVALID_VALUE, "tile_n: unsupported tile %d x %d (set tile first)", m->tile_m, value);
         m->tile_n = value;
     } else if (n == "profile") m->profile = value ? 1 : 0;
-    else return fail(PCD_INVALID_VALUE, "unknown option '%s'", name);
+    else if (n == "tile_order") {
+        if (value != TILE_INTERLEAVED && value != TILE_CONTIGUOUS)
+            return fail(PCD_INVALID_VALUE, "tile_order must be 0 (interleaved) or 1 (contiguous)");
+        m->tile_order = value;
+    } else return fail(PCD_INVALID_VALUE, "unknown option '%s'", name);
     // cached graphs were captured with the old options
     for (auto& w : m->ws) {
         for (auto& p : w->plans) {
