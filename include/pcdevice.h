@@ -202,6 +202,57 @@ int pcd_pc_relax_ragged(pcd_model* model, const float* x0_packed, const int* row
                         int requests, int exit_rule, float exit_threshold, int* steps_used,
                         float* out_top, float* out_energy, void* stream);
 
+/* Network.InferCore with the top clamped (Network.cs:75-111 with clampTop and a
+ * label; the settling of Network.InferEnergy, :234-244): layer 0 holds x0,
+ * layer levels-1 holds `top` and is never updated (Layer.cs:275), the hidden
+ * layers start at zero.  Device pointers:
+ *   x0          [batch x sizes[0]],  top [batch x sizes[levels-1]]
+ *   out_states  nullable; every layer as in pcd_pc_relax
+ *   out_energy  nullable; [steps x batch] per-sample energy of each step (the
+ *               last row is InferEnergy's ComputeEnergyCore)
+ * Errors as pcd_pc_relax.  Asynchronous on `stream`. */
+int pcd_pc_relax_clamped(pcd_model* model, const float* x0, const float* top, int batch, int steps,
+                         float* out_states, float* out_energy, void* stream);
+
+/* Minimum-energy classification of a batch: Network.ClassEnergies
+ * (Network.cs:253-278) and Network.PredictCore (:369-415) for every sample
+ * at once.  Each sample is settled C = sizes[levels-1] times, the top clamped
+ * to one-hot(c) and the hidden layers starting at zero (batch x C packed rows);
+ * F(x, c) is the energy of the last step.  The class is the first c with the
+ * smallest F (:395), and its energy is F(x, c*) (the reference re-runs the
+ * winner, :400-406, which repeats the same settling).  Device pointers, each
+ * nullable but not all null:
+ *   x0                  [batch x sizes[0]]
+ *   out_class_energies  [batch x C]   ClassEnergies
+ *   out_class           [batch]       Predict
+ *   out_energy          [batch]       PredictWithEnergy's energy
+ * Errors as pcd_pc_relax.  Asynchronous on `stream`. */
+int pcd_pc_classify(pcd_model* model, const float* x0, int batch, int steps, float* out_class_energies,
+                    int* out_class, float* out_energy, void* stream);
+
+/* Learning step, Network.Learn (Network.cs:139-155): settles with x0 and
+ * `labels` clamped (as pcd_pc_relax_clamped), then updates every layer's
+ * weights in place with Layer.UpdateWeights (Layer.cs:320-333), the last step's
+ * delta_l = f'(pre_l) * e_{l-1} and the settled states:
+ *   W_l += eta_w delta_l^T mu_l,  b_l += eta_w sum delta_l,  W_l -= eta_w weight_decay W_l.
+ * A batch applies the sum of its samples' updates, all taken at the weights
+ * the call starts from (batch = 1 is exactly Learn).  Device pointers:
+ *   x0 [batch x sizes[0]], labels [batch x sizes[levels-1]],
+ *   out_energy nullable [batch], each sample's energy at the last step.
+ * fp32 models only (PCD_NOT_SUPPORTED otherwise).  The model's weights change:
+ * no other call on the model may run concurrently (any stream).
+ * Asynchronous on `stream`. */
+int pcd_pc_learn(pcd_model* model, const float* x0, const float* labels, int batch, int steps, float eta_w,
+                 float weight_decay, float* out_energy, void* stream);
+
+/* Reads layer `layer`'s (1..levels-1) current weights back to host memory, as
+ * Network.ExportGenerativeSnapshot copies them (Network.cs:1328-1356):
+ *   W_out  nullable host [sizes[layer-1] x sizes[layer]] (16-bit models give
+ *          their operand values widened to fp32)
+ *   b_out  nullable host [sizes[layer-1]]
+ * Waits for the device. */
+int pcd_pc_model_get_weights(pcd_model* model, int layer, float* W_out, float* b_out);
+
 /* Model properties (levels, sizes, dtype) for host wrappers. */
 int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_sizes, int* dtype);
 

@@ -14,6 +14,10 @@
  *   PredicitiveCoding/Model/Layer.cs:273-309             UpdateState
  *   PredicitiveCoding/Model/Layer.cs:437-450             LocalEnergy
  *   PredicitiveCoding/Networks/Network.cs:75-131         InferCore + FFG
+ *   PredicitiveCoding/Networks/Network.cs:139-155        Learn
+ *   PredicitiveCoding/Networks/Network.cs:253-278        ClassEnergies
+ *   PredicitiveCoding/Networks/Network.cs:369-415        PredictCore (min-energy class)
+ *   PredicitiveCoding/Model/Layer.cs:320-333             UpdateWeights
  *   PredicitiveCoding/Networks/Network.cs:876-907        SettleAdaptive (exit rule)
  *   PredicitiveCoding/Networks/Network.cs:1080-1093      InferGetTop(resetState)
  *   PredicitiveCoding/Core/Activation.cs:34-132          f and f'
@@ -235,6 +239,7 @@ typedef struct {
     const float* b_all;   /* b_1..b_{L-1} concatenated */
     const float* prec;    /* [levels] */
     int round_mode;
+    int clamp_top;        /* layer L-1 held at its initial state (Network.cs:79-80, Layer.cs:275) */
 } model_t;
 
 static const float* w_of(const model_t* md, int l) {
@@ -267,7 +272,8 @@ static float* transpose(const float* w, int rows, int cols) {
  */
 static int relax_batch(const model_t* md, float** m, int batch, int steps,
                        int exit_rule, float exit_thr, float* energy_trace /* [steps x batch] or NULL */,
-                       float* final_energy /* total over the batch, or NULL */) {
+                       float* final_energy /* total over the batch, or NULL */,
+                       float** delta_out /* [levels], delta_out[l] [batch x s_{l-1}] of the last step, or NULL */) {
     int L = md->levels;
     const int* s = md->sizes;
     float** wT = calloc((size_t)L, sizeof(float*));
@@ -337,6 +343,8 @@ static int relax_batch(const model_t* md, float** m, int batch, int steps,
             size_t n = (size_t)batch * lower;
             pco_act_deriv_f32(md->act, pre[l], pred[l], delta, (long)n);
             for (size_t i = 0; i < n; i++) delta[i] *= e[l - 1][i];
+            if (delta_out) memcpy(delta_out[l], delta, sizeof(float) * n);
+            if (l == L - 1 && md->clamp_top) continue;                     /* Layer.cs:275 */
             gemm_mixed(delta, batch, lower, wr[l] ? wr[l] : w_of(md, l), size, g, md->round_mode, 1);
             float* state = m[l];
             const float* eself = l < L - 1 ? e[l] : NULL;
@@ -370,6 +378,7 @@ static void setup_model(model_t* md, const int* sizes, int levels, int act, floa
                         const float* W_all, const float* b_all, const float* prec, int round_mode) {
     md->levels = levels; md->sizes = sizes; md->act = act; md->eta = eta; md->act_reg = act_reg;
     md->ffg = ffg; md->W_all = W_all; md->b_all = b_all; md->prec = prec; md->round_mode = round_mode;
+    md->clamp_top = 0;
 }
 
 /*
@@ -391,7 +400,7 @@ int pco_batched_relax(const int* sizes, int levels, int act, float eta, float ac
     for (int l = 0; l < levels; l++) m[l] = calloc((size_t)batch * sizes[l], sizeof(float));
     memcpy(m[0], x0, sizeof(float) * (size_t)batch * sizes[0]);
     if (out_energy) memset(out_energy, 0, sizeof(float) * (size_t)steps * batch);
-    relax_batch(&md, m, batch, steps, EXIT_NONE, 0.f, out_energy, NULL);
+    relax_batch(&md, m, batch, steps, EXIT_NONE, 0.f, out_energy, NULL, NULL);
     memcpy(out_top, m[levels - 1], sizeof(float) * (size_t)batch * sizes[levels - 1]);
     if (out_states) {
         size_t off = 0;
@@ -429,12 +438,149 @@ int pco_ragged_relax(const int* sizes, int levels, int act, float eta, float act
         for (int l = 0; l < levels; l++) m[l] = calloc((size_t)nb * sizes[l], sizeof(float));
         memcpy(m[0], x0_packed + (size_t)r0 * s0, sizeof(float) * (size_t)nb * s0);
         float fe = 0.f;
-        steps_used[r] = relax_batch(&md, m, nb, steps[r], exit_rule, exit_thr, NULL, &fe);
+        steps_used[r] = relax_batch(&md, m, nb, steps[r], exit_rule, exit_thr, NULL, &fe, NULL);
         final_energy[r] = fe;
         memcpy(out_top + (size_t)r0 * sl, m[levels - 1], sizeof(float) * (size_t)nb * sl);
         for (int l = 0; l < levels; l++) free(m[l]);
         free(m);
     }
+    return 0;
+}
+
+/*
+ * InferCore with both ends clamped (Network.cs:75-111 with clampTop and a
+ * label): layer 0 holds x0, layer L-1 holds top [batch x s_{L-1}] and is never
+ * updated (Layer.cs:275), the hidden layers start at zero.  This is the
+ * settling inside Network.InferEnergy (:234-244), ClassEnergies (:253-278),
+ * PredictCore (:369-415) and Learn (:139-155).  Same outputs as
+ * pco_batched_relax.
+ */
+int pco_clamped_relax(const int* sizes, int levels, int act, float eta, float act_reg, int ffg,
+                      const float* W_all, const float* b_all, const float* prec, int round_mode,
+                      const float* x0, const float* top, int batch, int steps,
+                      float* out_states, float* out_energy) {
+    if (levels < 2 || batch < 1 || steps < 1) return -1;
+    model_t md;
+    setup_model(&md, sizes, levels, act, eta, act_reg, ffg, W_all, b_all, prec, round_mode);
+    md.clamp_top = 1;
+    float** m = calloc((size_t)levels, sizeof(float*));
+    for (int l = 0; l < levels; l++) m[l] = calloc((size_t)batch * sizes[l], sizeof(float));
+    memcpy(m[0], x0, sizeof(float) * (size_t)batch * sizes[0]);
+    memcpy(m[levels - 1], top, sizeof(float) * (size_t)batch * sizes[levels - 1]);
+    if (out_energy) memset(out_energy, 0, sizeof(float) * (size_t)steps * batch);
+    relax_batch(&md, m, batch, steps, EXIT_NONE, 0.f, out_energy, NULL, NULL);
+    if (out_states) {
+        size_t off = 0;
+        for (int l = 0; l < levels; l++) {
+            memcpy(out_states + off, m[l], sizeof(float) * (size_t)batch * sizes[l]);
+            off += (size_t)batch * sizes[l];
+        }
+    }
+    for (int l = 0; l < levels; l++) free(m[l]);
+    free(m);
+    return 0;
+}
+
+/*
+ * Minimum-energy classification, Network.PredictCore (Network.cs:369-415) and
+ * ClassEnergies (:253-278), one sample at a time as the reference runs it:
+ * for every class c the hidden states are zeroed, the top is clamped to
+ * one-hot(c) and the network settles for `steps` steps; F(x, c) is the energy
+ * of the last step's (pre-update) errors (ComputeEnergyCore, :939-945).  The
+ * class is the first c with the smallest F (strict <, :395); the winner's
+ * energy is F(x, c*) (the reference's re-run of the winner repeats the same
+ * deterministic settling).
+ *   class_energies [batch x C] (nullable), best_class [batch], best_energy [batch]
+ */
+int pco_classify(const int* sizes, int levels, int act, float eta, float act_reg, int ffg,
+                 const float* W_all, const float* b_all, const float* prec, int round_mode,
+                 const float* x0, int batch, int steps,
+                 float* class_energies, int* best_class, float* best_energy) {
+    if (levels < 2 || batch < 1 || steps < 1) return -1;
+    model_t md;
+    setup_model(&md, sizes, levels, act, eta, act_reg, ffg, W_all, b_all, prec, round_mode);
+    md.clamp_top = 1;
+    const int C = sizes[levels - 1], s0 = sizes[0];
+    float** m = calloc((size_t)levels, sizeof(float*));
+    for (int l = 0; l < levels; l++) m[l] = calloc((size_t)sizes[l], sizeof(float));
+    float* fc = malloc(sizeof(float) * (size_t)C);
+    for (int b = 0; b < batch; b++) {
+        float best = 3.402823466e38f;   /* float.MaxValue, :382 */
+        int bc = 0;
+        for (int c = 0; c < C; c++) {
+            for (int l = 1; l < levels; l++) memset(m[l], 0, sizeof(float) * sizes[l]);
+            memcpy(m[0], x0 + (size_t)b * s0, sizeof(float) * s0);
+            m[levels - 1][c] = 1.f;
+            float fe = 0.f;
+            relax_batch(&md, m, 1, steps, EXIT_NONE, 0.f, NULL, &fe, NULL);
+            fc[c] = fe;
+            if (class_energies) class_energies[(size_t)b * C + c] = fe;
+            if (fe < best) { best = fe; bc = c; }
+        }
+        best_class[b] = bc;
+        best_energy[b] = fc[bc];   /* the winner's re-run, :400-406 */
+    }
+    free(fc);
+    for (int l = 0; l < levels; l++) free(m[l]);
+    free(m);
+    return 0;
+}
+
+/*
+ * Learning step, Network.Learn (Network.cs:139-155): settle with input and
+ * label clamped, then for every layer l = 1..L-1 Layer.UpdateWeights
+ * (Layer.cs:320-333) with the last step's delta_l = f'(pre_l) . e_{l-1}
+ * (pre-update) and the settled (post-update) mu_l:
+ *   W_l += eta_w delta_l (x) mu_l ;  b_l += eta_w delta_l ;  W_l -= eta_w lambda W_l.
+ * A batch of B samples applies the sum of the B per-sample updates, all taken
+ * at the weights before the call (B = 1 is exactly Learn).
+ * W_all and b_all are updated in place; out_energy [batch] (nullable) is each
+ * sample's energy at the last step (the ComputeEnergy the trainer reads).
+ */
+int pco_learn(const int* sizes, int levels, int act, float eta, float act_reg, int ffg,
+              float* W_all, float* b_all, const float* prec,
+              const float* x0, const float* labels, int batch, int steps,
+              float eta_w, float weight_decay, float* out_energy) {
+    if (levels < 2 || batch < 1 || steps < 1) return -1;
+    model_t md;
+    setup_model(&md, sizes, levels, act, eta, act_reg, ffg, W_all, b_all, prec, ROUND_NONE);
+    md.clamp_top = 1;
+    const int L = levels;
+    float** m = calloc((size_t)L, sizeof(float*));
+    float** d = calloc((size_t)L, sizeof(float*));
+    for (int l = 0; l < L; l++) m[l] = calloc((size_t)batch * sizes[l], sizeof(float));
+    for (int l = 1; l < L; l++) d[l] = calloc((size_t)batch * sizes[l - 1], sizeof(float));
+    memcpy(m[0], x0, sizeof(float) * (size_t)batch * sizes[0]);
+    memcpy(m[L - 1], labels, sizeof(float) * (size_t)batch * sizes[L - 1]);
+    float* trace = calloc((size_t)steps * batch, sizeof(float));
+    relax_batch(&md, m, batch, steps, EXIT_NONE, 0.f, trace, NULL, d);
+    if (out_energy) memcpy(out_energy, trace + (size_t)(steps - 1) * batch, sizeof(float) * batch);
+    free(trace);
+    for (int l = 1; l < L; l++) {
+        float* W = (float*)w_of(&md, l);
+        float* bb = (float*)b_of(&md, l);
+        const int lo = sizes[l - 1], sz = sizes[l];
+        float* dW = calloc((size_t)lo * sz, sizeof(float));
+        float* db = calloc((size_t)lo, sizeof(float));
+        for (int r = 0; r < batch; r++) {                   /* OuterProduct(delta, mu), summed */
+            const float* dr = d[l] + (size_t)r * lo;
+            const float* mr = m[l] + (size_t)r * sz;
+            for (int i = 0; i < lo; i++) {
+                db[i] += dr[i];
+                for (int j = 0; j < sz; j++) dW[(size_t)i * sz + j] += dr[i] * mr[j];
+            }
+        }
+        const size_t nw = (size_t)lo * sz;
+        for (size_t k = 0; k < nw; k++) W[k] += eta_w * dW[k];
+        for (int i = 0; i < lo; i++) bb[i] += eta_w * db[i];
+        if (weight_decay > 0.f)
+            for (size_t k = 0; k < nw; k++) W[k] += (-eta_w * weight_decay) * W[k];
+        free(dW);
+        free(db);
+    }
+    for (int l = 0; l < L; l++) { free(m[l]); free(d[l]); }
+    free(m);
+    free(d);
     return 0;
 }
 
@@ -451,7 +597,8 @@ int pco_ragged_relax(const int* sizes, int levels, int act, float eta, float act
  */
 int pco_persample_relax_f64(const int* sizes, int levels, int act, double eta, double act_reg, int ffg,
                             const double* W_all, const double* b_all, const double* prec,
-                            const double* x0, int batch, int steps,
+                            const double* x0, const double* top /* [batch x s_{L-1}] clamped top, or NULL */,
+                            int batch, int steps,
                             double* out_top, double* out_states, double* out_energy) {
     if (levels < 2 || batch < 1 || steps < 1) return -1;
     int L = levels;
@@ -476,6 +623,7 @@ int pco_persample_relax_f64(const int* sizes, int levels, int act, double eta, d
     for (int smp = 0; smp < batch; smp++) {
         for (int l = 1; l < L; l++) memset(mu[l], 0, sizeof(double) * sizes[l]);   /* resetState */
         memcpy(mu[0], x0 + (size_t)smp * sizes[0], sizeof(double) * sizes[0]);    /* ClampLayer(0) */
+        if (top) memcpy(mu[L - 1], top + (size_t)smp * sizes[L - 1], sizeof(double) * sizes[L - 1]);
 
 #define PREDICT(l)                                                                       \
         do {                                                                             \
@@ -510,6 +658,7 @@ int pco_persample_relax_f64(const int* sizes, int levels, int act, double eta, d
             memset(e[L - 1], 0, sizeof(double) * sizes[L - 1]);
             if (out_energy) out_energy[(size_t)step * batch + smp] = etot;
             for (int l = 1; l < L; l++) {                                  /* UpdateState */
+                if (l == L - 1 && top) continue;                           /* clamped top, Layer.cs:275 */
                 const double* W_ = W_all + woff[l];
                 int lo = sizes[l - 1], sz = sizes[l];
                 double* grad = calloc((size_t)sz, sizeof(double));

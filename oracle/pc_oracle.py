@@ -59,8 +59,20 @@ def lib():
         L.pco_ragged_relax.restype = ctypes.c_int
         L.pco_persample_relax_f64.argtypes = [
             _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_int,
-            _f64p, _f64p, _f64p, _f64p, ctypes.c_int, ctypes.c_int, _f64p, _vp, _vp]
+            _f64p, _f64p, _f64p, _f64p, _vp, ctypes.c_int, ctypes.c_int, _f64p, _vp, _vp]
         L.pco_persample_relax_f64.restype = ctypes.c_int
+        L.pco_clamped_relax.argtypes = [
+            _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+            _f32p, _f32p, _f32p, ctypes.c_int, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _vp, _vp]
+        L.pco_clamped_relax.restype = ctypes.c_int
+        L.pco_classify.argtypes = [
+            _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+            _f32p, _f32p, _f32p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int, _f32p, _i32p, _f32p]
+        L.pco_classify.restype = ctypes.c_int
+        L.pco_learn.argtypes = [
+            _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+            _f32p, _f32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, _vp]
+        L.pco_learn.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -151,18 +163,21 @@ def batched_relax(sizes, act, eta, weights, biases, precisions, x0, steps,
 
 
 def persample_relax_f64(sizes, act, eta, weights, biases, precisions, x0, steps,
-                        act_reg=0.0, ffg=False, want_states=False, want_energy=False):
-    """Network.InferGetTop(x, steps, resetState: true) per sample, in float64."""
+                        act_reg=0.0, ffg=False, want_states=False, want_energy=False, top_clamp=None):
+    """Network.InferGetTop(x, steps, resetState: true) per sample, in float64;
+    with top_clamp [B, s_top] the top layer is held there (InferCore with a label)."""
     sizes = np.ascontiguousarray(sizes, dtype=np.int32)
     x0 = np.ascontiguousarray(x0, dtype=np.float64)
     B = x0.shape[0]
+    tc = None if top_clamp is None else np.ascontiguousarray(top_clamp, dtype=np.float64).reshape(B, int(sizes[-1]))
     top = np.empty((B, int(sizes[-1])), dtype=np.float64)
     states = np.empty(B * int(sizes.sum()), dtype=np.float64) if want_states else None
     energy = np.empty((steps, B), dtype=np.float64) if want_energy else None
     rc = lib().pco_persample_relax_f64(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg),
                                        _flat(weights, np.float64), _flat(biases, np.float64),
                                        np.ascontiguousarray(precisions, dtype=np.float64),
-                                       x0.ravel(), B, int(steps), top.ravel(), _ptr(states), _ptr(energy))
+                                       x0.ravel(), _ptr(tc), B, int(steps), top.ravel(), _ptr(states),
+                                       _ptr(energy))
     if rc != 0:
         raise ValueError("oracle rejected arguments")
     st = None
@@ -192,3 +207,75 @@ def ragged_relax(sizes, act, eta, weights, biases, precisions, x0_packed, row_of
     if rc != 0:
         raise ValueError("oracle rejected arguments")
     return used, fe, top
+
+
+def _split_states(states, sizes, B):
+    st, off = [], 0
+    for sz in sizes:
+        st.append(states[off:off + B * int(sz)].reshape(B, int(sz)))
+        off += B * int(sz)
+    return st
+
+
+def clamped_relax(sizes, act, eta, weights, biases, precisions, x0, top, steps,
+                  act_reg=0.0, ffg=False, round_mode="none"):
+    """InferCore with input and top clamped (Network.cs:75-111, clampTop).
+    Returns (states list, energy [T, B])."""
+    sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+    x0 = np.ascontiguousarray(x0, dtype=np.float32)
+    B = x0.shape[0]
+    top = np.ascontiguousarray(top, dtype=np.float32).reshape(B, int(sizes[-1]))
+    states = np.empty(B * int(sizes.sum()), dtype=np.float32)
+    energy = np.empty((steps, B), dtype=np.float32)
+    rc = lib().pco_clamped_relax(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg),
+                                 _flat(weights, np.float32), _flat(biases, np.float32),
+                                 np.ascontiguousarray(precisions, dtype=np.float32), ROUND[round_mode],
+                                 x0.ravel(), top.ravel(), B, int(steps), _ptr(states), _ptr(energy))
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    return _split_states(states, sizes, B), energy
+
+
+def classify(sizes, act, eta, weights, biases, precisions, x0, steps, act_reg=0.0, ffg=False, round_mode="none"):
+    """Network.PredictCore / ClassEnergies per sample: returns
+    (class_energies [B, C], best_class [B], best_energy [B])."""
+    sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+    x0 = np.ascontiguousarray(x0, dtype=np.float32)
+    B, C = x0.shape[0], int(sizes[-1])
+    ce = np.empty((B, C), dtype=np.float32)
+    bc = np.empty(B, dtype=np.int32)
+    be = np.empty(B, dtype=np.float32)
+    rc = lib().pco_classify(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg),
+                            _flat(weights, np.float32), _flat(biases, np.float32),
+                            np.ascontiguousarray(precisions, dtype=np.float32), ROUND[round_mode],
+                            x0.ravel(), B, int(steps), ce.ravel(), bc, be)
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    return ce, bc, be
+
+
+def learn(sizes, act, eta, weights, biases, precisions, x0, labels, steps, eta_w, weight_decay=0.0,
+          act_reg=0.0, ffg=False):
+    """Network.Learn on a batch (B = 1 is the reference call; B > 1 sums the
+    per-sample updates at the pre-call weights).  Returns (new weights, new
+    biases, energy [B])."""
+    sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+    x0 = np.ascontiguousarray(x0, dtype=np.float32)
+    B = x0.shape[0]
+    labels = np.ascontiguousarray(labels, dtype=np.float32).reshape(B, int(sizes[-1]))
+    W = _flat(weights, np.float32).copy()
+    b = _flat(biases, np.float32).copy()
+    energy = np.empty(B, dtype=np.float32)
+    rc = lib().pco_learn(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg), W, b,
+                         np.ascontiguousarray(precisions, dtype=np.float32), x0.ravel(), labels.ravel(),
+                         B, int(steps), float(eta_w), float(weight_decay), _ptr(energy))
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    new_w, new_b, wo, bo = [], [], 0, 0
+    for l in range(1, len(sizes)):
+        lo, sz = int(sizes[l - 1]), int(sizes[l])
+        new_w.append(W[wo:wo + lo * sz].reshape(lo, sz))
+        new_b.append(b[bo:bo + lo])
+        wo += lo * sz
+        bo += lo
+    return new_w, new_b, energy

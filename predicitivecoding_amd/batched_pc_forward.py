@@ -153,6 +153,117 @@ class PcDeviceModel:
         return used, fe, top_h
 
 
+    # ------------------------------------- clamped settling, classes, learning
+
+    def _batch_in(self, x, cols, name):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != cols:
+            raise ArgumentException(f"{name} must be [batch x {cols}]")
+        if x.shape[0] < 1:
+            raise ArgumentException("Empty batch.")
+        return x
+
+    def _sync(self, stream):
+        if stream:
+            stream.synchronize()
+        else:
+            call("pcd_device_synchronize")
+
+    def relax_clamped(self, x0: np.ndarray, top: np.ndarray, steps: int, want_states: bool = False,
+                      stream: Stream | None = None):
+        """pcd_pc_relax_clamped on host arrays: input and top clamped (Network.InferCore
+        with a label).  Returns (states list or None, energy [steps x batch])."""
+        x0 = self._batch_in(x0, self.sizes[0], "inputs")
+        B = x0.shape[0]
+        top = np.ascontiguousarray(top, dtype=np.float32).reshape(B, self.sizes[-1])
+        if steps < 1:
+            raise ArgumentOutOfRangeException("inferenceSteps")
+        dx, dt = DeviceTensor.from_host(x0), DeviceTensor.from_host(top)
+        st = DeviceTensor((B * sum(self.sizes),)) if want_states else None
+        en = DeviceTensor((steps, B))
+        try:
+            call("pcd_pc_relax_clamped", self.handle, dx.ptr, dt.ptr, B, int(steps), st.ptr if st else None, en.ptr,
+                 stream.handle if stream else None)
+            self._sync(stream)
+            states = None
+            if st is not None:
+                flat, states, off = st.to_host(), [], 0
+                for s in self.sizes:
+                    states.append(flat[off:off + B * s].reshape(B, s))
+                    off += B * s
+            energy = en.to_host()
+        finally:
+            for t in (dx, dt, st, en):
+                if t is not None:
+                    t.free()
+        return states, energy
+
+    def classify_device(self, x0_ptr: int, batch: int, steps: int, class_energies_ptr: int | None = None,
+                        class_ptr: int | None = None, energy_ptr: int | None = None,
+                        stream: Stream | None = None) -> None:
+        """pcd_pc_classify on device pointers, queued on `stream` (no sync)."""
+        call("pcd_pc_classify", self.handle, x0_ptr, int(batch), int(steps), class_energies_ptr, class_ptr,
+             energy_ptr, stream.handle if stream else None)
+
+    def classify(self, x0: np.ndarray, steps: int, stream: Stream | None = None):
+        """Minimum-energy classification of a host batch (Network.ClassEnergies and
+        PredictWithEnergy per sample).  Returns (class_energies [B x C], class [B],
+        energy [B])."""
+        x0 = self._batch_in(x0, self.sizes[0], "inputs")
+        if steps < 1:
+            raise ArgumentOutOfRangeException("inferenceSteps")
+        B, C = x0.shape[0], self.sizes[-1]
+        dx = DeviceTensor.from_host(x0)
+        ce = DeviceTensor((B, C))
+        cls = DeviceTensor((B,), dtype=np.int32)
+        be = DeviceTensor((B,))
+        try:
+            self.classify_device(dx.ptr, B, steps, ce.ptr, cls.ptr, be.ptr, stream)
+            self._sync(stream)
+            out = ce.to_host(), cls.to_host(), be.to_host()
+        finally:
+            for t in (dx, ce, cls, be):
+                t.free()
+        return out
+
+    def learn_device(self, x0_ptr: int, labels_ptr: int, batch: int, steps: int, eta_w: float,
+                     weight_decay: float = 0.0, energy_ptr: int | None = None, stream: Stream | None = None) -> None:
+        """pcd_pc_learn on device pointers, queued on `stream` (no sync)."""
+        call("pcd_pc_learn", self.handle, x0_ptr, labels_ptr, int(batch), int(steps), float(eta_w),
+             float(weight_decay), energy_ptr, stream.handle if stream else None)
+
+    def learn(self, x0: np.ndarray, labels: np.ndarray, steps: int, eta_w: float, weight_decay: float = 0.0,
+              stream: Stream | None = None) -> np.ndarray:
+        """Network.Learn on a host batch (the sum of the per-sample updates);
+        returns each sample's energy at the last step."""
+        x0 = self._batch_in(x0, self.sizes[0], "inputs")
+        B = x0.shape[0]
+        labels = np.ascontiguousarray(labels, dtype=np.float32).reshape(B, self.sizes[-1])
+        if steps < 1:
+            raise ArgumentOutOfRangeException("inferenceSteps")
+        dx, dl = DeviceTensor.from_host(x0), DeviceTensor.from_host(labels)
+        en = DeviceTensor((B,))
+        try:
+            self.learn_device(dx.ptr, dl.ptr, B, steps, eta_w, weight_decay, en.ptr, stream)
+            self._sync(stream)
+            energy = en.to_host()
+        finally:
+            for t in (dx, dl, en):
+                t.free()
+        return energy
+
+    def get_weights(self):
+        """Current (W_l, b_l) of every layer l = 1..L-1 as host arrays."""
+        W, b = [], []
+        for l in range(1, len(self.sizes)):
+            w = np.empty((self.sizes[l - 1], self.sizes[l]), dtype=np.float32)
+            v = np.empty(self.sizes[l - 1], dtype=np.float32)
+            call("pcd_pc_model_get_weights", self.handle, l, w.ctypes.data, v.ctypes.data)
+            W.append(w)
+            b.append(v)
+        return W, b
+
+
 class BatchedPcForward:
     """Drop-in for the reference's static class (BatchedPcForward.cs:28-139)."""
 

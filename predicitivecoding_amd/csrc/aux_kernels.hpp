@@ -74,4 +74,74 @@ __global__ void exit_kernel(const float* __restrict__ part, int ldp, int nslots,
     }
 }
 
+// Row energies of a step from the per-slot partials when no update-phase
+// launch is there to reduce them (every free layer clamped).
+__global__ void energy_rows_kernel(const float* __restrict__ part, int ldp, int nslots, float* __restrict__ out,
+                                   int rows) {
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+        float s = 0.f;
+        for (int k = 0; k < nslots; ++k) s += part[(size_t)k * ldp + r];
+        out[r] = s;
+    }
+}
+
+// Layer-0 rows of a classification batch: row r is sample r / classes of x0
+// ([batch x cols], packed), copied into the fp32 state [rows x ld].
+__global__ void replicate_rows_kernel(const float* __restrict__ x0, int cols, int classes, int rows,
+                                      float* __restrict__ dst, int ld) {
+    const size_t n = (size_t)rows * cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i / cols), c = (int)(i % cols);
+        dst[(size_t)r * ld + c] = x0[(size_t)(r / classes) * cols + c];
+    }
+}
+
+// Clamped top rows: from src ([rows x cols], packed) or, with src null, the
+// one-hot of class r % cols (ClassEnergies' candidate label), written to the
+// fp32 state [rows x ld] and, when dst_op is set, to its operand-type copy.
+// Columns cols..ld-1 are written zero.
+template <typename OP>
+__global__ void top_rows_kernel(const float* __restrict__ src, int cols, int rows, float* __restrict__ dst,
+                                void* __restrict__ dst_op, int ld) {
+    const size_t n = (size_t)rows * ld;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i / ld), c = (int)(i % ld);
+        float v = 0.f;
+        if (c < cols) v = src ? src[(size_t)r * cols + c] : (c == r % cols ? 1.f : 0.f);
+        dst[i] = v;
+        if (dst_op) OpTraits<OP>::store(dst_op, i, v);
+    }
+}
+
+// Minimum-energy class per sample (Network.PredictCore, Network.cs:385-396):
+// the first class with the smallest energy.  e holds the [batch x classes]
+// last-step energies; the per-class table, the class and its energy are written
+// where the pointers are set.
+__global__ void class_argmin_kernel(const float* __restrict__ e, int batch, int classes, float* __restrict__ table,
+                                    int* __restrict__ cls, float* __restrict__ best) {
+    for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < batch; b += gridDim.x * blockDim.x) {
+        float be = 3.402823466e38f;   // float.MaxValue
+        int bc = 0;
+        for (int c = 0; c < classes; ++c) {
+            const float v = e[(size_t)b * classes + c];
+            if (table) table[(size_t)b * classes + c] = v;
+            if (v < be) { be = v; bc = c; }
+        }
+        if (cls) cls[b] = bc;
+        // the winner's energy as the reference's re-run of the winning class returns it
+        if (best) best[b] = e[(size_t)b * classes + bc];
+    }
+}
+
+// Bias step of the learning rule (Layer.cs:327): b[i] += eta_w * sum over the
+// batch rows of D[r][i], rows summed in order.
+__global__ void bias_update_kernel(const float* __restrict__ d, int ld, int rows, int cols, float* __restrict__ bias,
+                                   float eta_w) {
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x) {
+        float s = 0.f;
+        for (int r = 0; r < rows; ++r) s += d[(size_t)r * ld + c];
+        bias[c] += eta_w * s;
+    }
+}
+
 }  // namespace pcd

@@ -234,7 +234,7 @@ struct Workspace {
 };
 
 struct Plan {
-    int batch = 0, steps = 0, want_energy = 0, ffg = 0;
+    int batch = 0, steps = 0, want_energy = 0, clamp_top = 0;
     Tile tile{0, 0};
     float* energy_out = nullptr;       // [steps x batch]
     hipGraphExec_t exec = nullptr;
@@ -382,7 +382,7 @@ const void* state_operand(const pcd_model* m, const Workspace* w, int l) {
 
 // Problem sets of the two phases for a batch; problems beyond kMaxProblems
 // spill into further sets (still one phase: the problems are independent).
-void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile tile, int ragged,
+void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile tile, int clamp_top,
                       std::vector<ProblemSet>& err, std::vector<ProblemSet>& upd, int* nslots) {
     err.clear();
     upd.clear();
@@ -414,6 +414,7 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         slot += p.tiles_n * slots_per_tile_n(tile);
     }
     for (int l = 1; l < L; ++l) {
+        if (l == L - 1 && clamp_top) break;   // a clamped top is never updated (Layer.cs:275)
         if (upd.empty() || upd.back().n == kMaxProblems) { upd.emplace_back(); upd.back().n = 0; }
         ProblemSet& ps = upd.back();
         Problem& p = ps.p[ps.n++];
@@ -433,7 +434,6 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         p.mop = m->dtype == PCD_F32 ? nullptr : w->S[l];
         p.eself = l <= L - 2 ? w->E[l] : nullptr;
     }
-    (void)ragged;
     *nslots = slot;
 }
 
@@ -452,8 +452,23 @@ PhaseArgs base_args(const pcd_model* m, const Workspace* w, int batch, int nslot
     return a;
 }
 
-// Zero the free states, FFG warm start (Network.cs:121-131), then the step loop.
-// With `events` set, each phase launch is bracketed by HIP events (eager only).
+// One settling to enqueue: rows, steps, tile and the per-call variants.
+struct RelaxSpec {
+    int batch = 0, steps = 0;
+    Tile tile{0, 0};
+    int clamp_top = 0;              // layer L-1 holds rows staged by the caller and is never updated
+    float* energy_out = nullptr;    // [steps x batch] per-row energies (nullable)
+    // ragged early exit (row_req null: fixed steps for every row)
+    const int* row_req = nullptr;
+    int* done_at = nullptr;
+    const int* row_offsets = nullptr;
+    int requests = 0, exit_rule = 0;
+    float exit_thr = 0.f;
+    float* prev_energy = nullptr;
+    float* last_energy = nullptr;
+};
+
+// With a timer, each phase launch is bracketed by HIP events (eager only).
 struct PhaseTimer {
     std::vector<std::pair<hipEvent_t, hipEvent_t>> err, upd;
 };
@@ -482,22 +497,25 @@ int collect_timer(pcd_model* m, PhaseTimer& timer, hipStream_t s) {
     return PCD_SUCCESS;
 }
 
-int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, Tile tile, float* energy_out,
-                  const int* row_req, int* done_at, const int* row_offsets_dev, int requests, int exit_rule,
-                  float exit_thr, float* prev_energy, float* last_energy, hipStream_t s, PhaseTimer* timer) {
+// Zero the free states, FFG warm start (Network.cs:121-131), then the step
+// loop.  Layer 0 (and, with clamp_top, layer L-1) must already hold its rows.
+int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s, PhaseTimer* timer) {
     const int L = m->L;
+    const int batch = r.batch;
+    const Tile tile = r.tile;
     int st;
     for (int l = 1; l < L; ++l) {
+        if (l == L - 1 && r.clamp_top) break;
         if ((st = launch_zero(w->M[l], (size_t)w->cap * m->P[l] * 4, s))) return st;
         if (w->S[l] && (st = launch_zero(w->S[l], (size_t)w->cap * m->P[l] * op_bytes(m->dtype), s))) return st;
     }
     std::vector<ProblemSet> err, upd;
     int nslots = 0;
-    build_phase_sets(m, w, batch, tile, row_req != nullptr, err, upd, &nslots);
+    build_phase_sets(m, w, batch, tile, r.clamp_top, err, upd, &nslots);
     PhaseArgs args = base_args(m, w, batch, nslots);
-    args.row_req = row_req;
-    args.done_at = done_at;
-    const bool need_energy = energy_out != nullptr || row_req != nullptr;
+    args.row_req = r.row_req;
+    args.done_at = r.done_at;
+    const bool need_energy = r.energy_out != nullptr || r.row_req != nullptr;
     if (!need_energy) args.energy_part = nullptr;
 
     if (m->ffg) {
@@ -525,7 +543,7 @@ int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, Tile tile, f
             if ((st = launch_phase(m->dtype, tile, EPI_FFG, ps, fa, s))) return st;
         }
     }
-    for (int t = 0; t < steps; ++t) {
+    for (int t = 0; t < r.steps; ++t) {
         PhaseArgs a = args;
         a.t = t;
         a.energy_out = nullptr;
@@ -539,12 +557,20 @@ int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, Tile tile, f
         for (auto& ps : err)
             if ((st = launch_phase(m->dtype, tile, EPI_ERROR, ps, a, s))) return st;
         if (timer) HIP_TRY(hipEventRecord(e1, s));
-        if (row_req) {
-            hipLaunchKernelGGL(exit_kernel, dim3(requests), dim3(256), 0, s, (const float*)w->energy_part, w->cap,
-                               nslots, row_offsets_dev, done_at, prev_energy, last_energy, t, exit_rule, exit_thr);
+        if (r.row_req) {
+            hipLaunchKernelGGL(exit_kernel, dim3(r.requests), dim3(256), 0, s, (const float*)w->energy_part, w->cap,
+                               nslots, r.row_offsets, r.done_at, r.prev_energy, r.last_energy, t, r.exit_rule,
+                               r.exit_thr);
             if ((st = from_hip(hipGetLastError(), "exit_kernel launch"))) return st;
         }
-        a.energy_out = energy_out;
+        a.energy_out = r.energy_out;
+        if (upd.empty() && r.energy_out) {
+            // No free layer to update: reduce the step's row energies on their own.
+            const int grid = std::min((batch + 255) / 256, 1024);
+            hipLaunchKernelGGL(energy_rows_kernel, dim3(grid), dim3(256), 0, s, (const float*)w->energy_part,
+                               w->cap, nslots, r.energy_out + (size_t)t * batch, batch);
+            if ((st = from_hip(hipGetLastError(), "energy_rows_kernel launch"))) return st;
+        }
         bool first = true;
         for (auto& ps : upd) {
             PhaseArgs ua = a;
@@ -561,11 +587,12 @@ int enqueue_relax(pcd_model* m, Workspace* w, int batch, int steps, Tile tile, f
     return PCD_SUCCESS;
 }
 
-Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy, Tile tile, int* status) {
+Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy, int clamp_top, Tile tile,
+               int* status) {
     *status = PCD_SUCCESS;
     for (auto& p : w->plans)
-        if (p->batch == batch && p->steps == steps && p->want_energy == want_energy && p->tile.m == tile.m &&
-            p->tile.n == tile.n) {
+        if (p->batch == batch && p->steps == steps && p->want_energy == want_energy && p->clamp_top == clamp_top &&
+            p->tile.m == tile.m && p->tile.n == tile.n) {
             p->last_use = ++m->clock;
             return p.get();
         }
@@ -581,6 +608,7 @@ Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy
     p->batch = batch;
     p->steps = steps;
     p->want_energy = want_energy;
+    p->clamp_top = clamp_top;
     p->tile = tile;
     p->last_use = ++m->clock;
     if (want_energy) {
@@ -591,8 +619,13 @@ Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy
         hipStream_t cs = w->capture;
         hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
         if (e != hipSuccess) { *status = from_hip(e, "hipStreamBeginCapture"); return nullptr; }
-        int st = enqueue_relax(m, w, batch, steps, tile, p->energy_out, nullptr, nullptr, nullptr, 0, 0, 0.f,
-                               nullptr, nullptr, cs, nullptr);
+        RelaxSpec r;
+        r.batch = batch;
+        r.steps = steps;
+        r.tile = tile;
+        r.clamp_top = clamp_top;
+        r.energy_out = p->energy_out;
+        int st = enqueue_relax(m, w, r, cs, nullptr);
         hipGraph_t g = nullptr;
         e = hipStreamEndCapture(cs, &g);
         if (st) { if (g) (void)hipGraphDestroy(g); *status = st; return nullptr; }
@@ -603,6 +636,41 @@ Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy
     }
     w->plans.push_back(std::move(p));
     return w->plans.back().get();
+}
+
+// A fixed-step settling of `batch` staged rows (layer 0, and the top with
+// clamp_top): eager with per-phase timing under the profile option, else the
+// cached graph of the T-step loop.  *energy receives the buffer holding the
+// [steps x batch] row energies when want_energy is set (the caller's
+// `caller_energy` or the plan's own), valid once the stream reaches it.
+int run_relax(pcd_model* m, Workspace* w, int batch, int steps, int clamp_top, int want_energy, float* caller_energy,
+              hipStream_t s, const float** energy) {
+    RelaxSpec r;
+    r.batch = batch;
+    r.steps = steps;
+    r.tile = choose_tile(m, batch);
+    r.clamp_top = clamp_top;
+    *energy = nullptr;
+    if (m->profile || !m->use_graph) {
+        float* buf = caller_energy;
+        if (want_energy && !buf) return fail(PCD_INVALID_VALUE, "run_relax: energy buffer missing");
+        r.energy_out = want_energy ? buf : nullptr;
+        PhaseTimer timer;
+        int st = enqueue_relax(m, w, r, s, m->profile ? &timer : nullptr);
+        if (m->profile) {
+            int st2 = collect_timer(m, timer, s);
+            if (!st) st = st2;
+        }
+        if (st) return st;
+        *energy = r.energy_out;
+        return PCD_SUCCESS;
+    }
+    int st = PCD_SUCCESS;
+    Plan* p = get_plan(m, w, batch, steps, want_energy, clamp_top, r.tile, &st);
+    if (!p) return st;
+    HIP_TRY(hipGraphLaunch(p->exec, s));
+    *energy = p->energy_out;
+    return PCD_SUCCESS;
 }
 
 int check_model(pcd_model* m) {
@@ -1037,6 +1105,16 @@ static int copy_out_rows(float* dst, int cols, const float* src, int ld, int row
     return PCD_SUCCESS;
 }
 
+// Copies every layer's first `batch` rows, layer after layer, into out_states.
+static int copy_out_states(pcd_model* m, Workspace* w, float* out_states, int batch, hipStream_t s) {
+    size_t off = 0;
+    for (int l = 0; l < m->L; ++l) {
+        if (int st = copy_out_rows(out_states + off, m->s[l], w->M[l], m->P[l], batch, s)) return st;
+        off += (size_t)batch * m->s[l];
+    }
+    return PCD_SUCCESS;
+}
+
 int pcd_pc_relax(pcd_model* m, const float* x0, int batch, int steps, float* out_top, float* out_states,
                  float* out_energy, void* stream_) {
     if (int st = check_model(m)) return st;
@@ -1049,39 +1127,15 @@ int pcd_pc_relax(pcd_model* m, const float* x0, int batch, int steps, float* out
     Workspace* w = nullptr;
     if (int st = ensure_workspace(m, s, batch, &w)) return st;
     const int L = m->L;
-    const Tile tile = choose_tile(m, batch);
     HIP_TRY(hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, batch,
                              hipMemcpyDeviceToDevice, s));
-    float* energy_dst = nullptr;
-    if (m->profile) {
-        // Eager run with per-phase events; the energy buffer is the caller's.
-        PhaseTimer timer;
-        int st = enqueue_relax(m, w, batch, steps, tile, out_energy, nullptr, nullptr, nullptr, 0, 0, 0.f, nullptr,
-                               nullptr, s, &timer);
-        int st2 = collect_timer(m, timer, s);
-        if (st) return st;
-        if (st2) return st2;
-    } else if (m->use_graph) {
-        int st = PCD_SUCCESS;
-        Plan* p = get_plan(m, w, batch, steps, out_energy != nullptr, tile, &st);
-        if (!p) return st;
-        HIP_TRY(hipGraphLaunch(p->exec, s));
-        energy_dst = p->energy_out;
-    } else {
-        int st = enqueue_relax(m, w, batch, steps, tile, out_energy, nullptr, nullptr, nullptr, 0, 0, 0.f, nullptr,
-                               nullptr, s, nullptr);
-        if (st) return st;
-    }
+    const float* energy = nullptr;
+    if (int st = run_relax(m, w, batch, steps, 0, out_energy != nullptr, out_energy, s, &energy)) return st;
     if (int st = copy_out_rows(out_top, m->s[L - 1], w->M[L - 1], m->P[L - 1], batch, s)) return st;
-    if (out_states) {
-        size_t off = 0;
-        for (int l = 0; l < L; ++l) {
-            if (int st = copy_out_rows(out_states + off, m->s[l], w->M[l], m->P[l], batch, s)) return st;
-            off += (size_t)batch * m->s[l];
-        }
-    }
-    if (out_energy && energy_dst)
-        HIP_TRY(hipMemcpyAsync(out_energy, energy_dst, (size_t)steps * batch * 4, hipMemcpyDeviceToDevice, s));
+    if (out_states)
+        if (int st = copy_out_states(m, w, out_states, batch, s)) return st;
+    if (out_energy && energy != out_energy)
+        HIP_TRY(hipMemcpyAsync(out_energy, energy, (size_t)steps * batch * 4, hipMemcpyDeviceToDevice, s));
     return PCD_SUCCESS;
 }
 
@@ -1135,8 +1189,19 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
         // With the profile option, every phase launch is timed (the ragged
         // loop always runs eagerly).
         PhaseTimer timer;
-        st = enqueue_relax(m, w, rows, tmax, tile, nullptr, d_row_req, d_done, d_offsets, requests, exit_rule,
-                           exit_threshold, d_prev, d_last, s, m->profile ? &timer : nullptr);
+        RelaxSpec r;
+        r.batch = rows;
+        r.steps = tmax;
+        r.tile = tile;
+        r.row_req = d_row_req;
+        r.done_at = d_done;
+        r.row_offsets = d_offsets;
+        r.requests = requests;
+        r.exit_rule = exit_rule;
+        r.exit_thr = exit_threshold;
+        r.prev_energy = d_prev;
+        r.last_energy = d_last;
+        st = enqueue_relax(m, w, r, s, m->profile ? &timer : nullptr);
         if (m->profile) {
             int st2 = collect_timer(m, timer, s);
             if (!st) st = st2;
@@ -1153,6 +1218,232 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
     if (!st && out_energy) std::memcpy(out_energy, last.data(), (size_t)requests * 4);
     pool_free(tables, s);
     return st;
+}
+
+// ------------------------------------------- clamped settling, classes, learning
+
+// Writes the clamped top rows of a settling: src [rows x s_top] packed, or,
+// with src null, the one-hot label of class r % s_top for row r.
+static int stage_top(pcd_model* m, Workspace* w, const float* src, int rows, hipStream_t s) {
+    const int lt = m->L - 1;
+    const size_t n = (size_t)rows * m->P[lt];
+    const int grid = (int)std::min<size_t>((n + 255) / 256, 8192);
+    switch (m->dtype) {
+    case PCD_F32:
+        hipLaunchKernelGGL(top_rows_kernel<float>, dim3(grid), dim3(256), 0, s, src, m->s[lt], rows, w->M[lt],
+                           nullptr, m->P[lt]);
+        break;
+    case PCD_BF16:
+        hipLaunchKernelGGL(top_rows_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, src, m->s[lt], rows, w->M[lt],
+                           w->S[lt], m->P[lt]);
+        break;
+    default:
+        hipLaunchKernelGGL(top_rows_kernel<f16_t>, dim3(grid), dim3(256), 0, s, src, m->s[lt], rows, w->M[lt],
+                           w->S[lt], m->P[lt]);
+        break;
+    }
+    return from_hip(hipGetLastError(), "top_rows_kernel launch");
+}
+
+int pcd_pc_relax_clamped(pcd_model* m, const float* x0, const float* top, int batch, int steps, float* out_states,
+                         float* out_energy, void* stream_) {
+    if (int st = check_model(m)) return st;
+    if (batch < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
+    if (steps < 1) return fail(PCD_INVALID_VALUE, "inferenceSteps must be >= 1, got %d", steps);
+    if (!x0 || !top) return fail(PCD_INVALID_VALUE, "pcd_pc_relax_clamped: null pointer");
+    hipStream_t s = (hipStream_t)stream_;
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    Workspace* w = nullptr;
+    if (int st = ensure_workspace(m, s, batch, &w)) return st;
+    HIP_TRY(hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, batch,
+                             hipMemcpyDeviceToDevice, s));
+    if (int st = stage_top(m, w, top, batch, s)) return st;
+    const float* energy = nullptr;
+    if (int st = run_relax(m, w, batch, steps, 1, out_energy != nullptr, out_energy, s, &energy)) return st;
+    if (out_states)
+        if (int st = copy_out_states(m, w, out_states, batch, s)) return st;
+    if (out_energy && energy != out_energy)
+        HIP_TRY(hipMemcpyAsync(out_energy, energy, (size_t)steps * batch * 4, hipMemcpyDeviceToDevice, s));
+    return PCD_SUCCESS;
+}
+
+int pcd_pc_classify(pcd_model* m, const float* x0, int batch, int steps, float* out_class_energies, int* out_class,
+                    float* out_energy, void* stream_) {
+    if (int st = check_model(m)) return st;
+    if (batch < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
+    if (steps < 1) return fail(PCD_INVALID_VALUE, "inferenceSteps must be >= 1, got %d", steps);
+    if (!x0) return fail(PCD_INVALID_VALUE, "pcd_pc_classify: null input");
+    if (!out_class_energies && !out_class && !out_energy)
+        return fail(PCD_INVALID_VALUE, "pcd_pc_classify: no output requested");
+    const int C = m->s[m->L - 1];
+    const long rows_l = (long)batch * C;
+    if (rows_l > (1L << 30)) return fail(PCD_INVALID_VALUE, "pcd_pc_classify: %d x %d rows is too many", batch, C);
+    const int rows = (int)rows_l;
+    hipStream_t s = (hipStream_t)stream_;
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    Workspace* w = nullptr;
+    if (int st = ensure_workspace(m, s, rows, &w)) return st;
+    {
+        const size_t n = (size_t)rows * m->s[0];
+        const int grid = (int)std::min<size_t>((n + 255) / 256, 8192);
+        hipLaunchKernelGGL(replicate_rows_kernel, dim3(grid), dim3(256), 0, s, x0, m->s[0], C, rows, w->M[0],
+                           m->P[0]);
+        if (int st = from_hip(hipGetLastError(), "replicate_rows_kernel launch")) return st;
+    }
+    if (int st = stage_top(m, w, nullptr, rows, s)) return st;
+    // Eager runs write the energies into a stream-ordered scratch buffer.
+    void* scratch = nullptr;
+    if (m->profile || !m->use_graph)
+        if (int st = pool_alloc(&scratch, (size_t)steps * rows * 4, s)) return st;
+    const float* energy = nullptr;
+    int st = run_relax(m, w, rows, steps, 1, 1, (float*)scratch, s, &energy);
+    if (!st) {
+        const int grid = std::min((batch + 255) / 256, 1024);
+        hipLaunchKernelGGL(class_argmin_kernel, dim3(grid), dim3(256), 0, s, energy + (size_t)(steps - 1) * rows,
+                           batch, C, out_class_energies, out_class, out_energy);
+        st = from_hip(hipGetLastError(), "class_argmin_kernel launch");
+    }
+    if (scratch) {
+        int st2 = pool_free(scratch, s);
+        if (!st) st = st2;
+    }
+    return st;
+}
+
+int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, int steps, float eta_w,
+                 float weight_decay, float* out_energy, void* stream_) {
+    if (int st = check_model(m)) return st;
+    if (batch < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
+    if (steps < 1) return fail(PCD_INVALID_VALUE, "inferenceSteps must be >= 1, got %d", steps);
+    if (!x0 || !labels) return fail(PCD_INVALID_VALUE, "pcd_pc_learn: null pointer");
+    if (m->dtype != PCD_F32)
+        return fail(PCD_NOT_SUPPORTED, "pcd_pc_learn: the learning step updates fp32 weights (model is 16-bit)");
+    hipStream_t s = (hipStream_t)stream_;
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    Workspace* w = nullptr;
+    if (int st = ensure_workspace(m, s, batch, &w)) return st;
+    const int L = m->L;
+    HIP_TRY(hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, batch,
+                             hipMemcpyDeviceToDevice, s));
+    if (int st = stage_top(m, w, labels, batch, s)) return st;
+    void* scratch = nullptr;
+    const bool want_energy = out_energy != nullptr;
+    if (want_energy && (m->profile || !m->use_graph))
+        if (int st = pool_alloc(&scratch, (size_t)steps * batch * 4, s)) return st;
+    const float* energy = nullptr;
+    int st = run_relax(m, w, batch, steps, 1, want_energy, (float*)scratch, s, &energy);
+    if (!st && want_energy) {
+        hipError_t e = hipMemcpyAsync(out_energy, energy + (size_t)(steps - 1) * batch, (size_t)batch * 4,
+                                      hipMemcpyDeviceToDevice, s);
+        st = from_hip(e, "learn energy copy");
+    }
+
+    // Hebbian step of every layer (Layer.UpdateWeights, Layer.cs:320-333):
+    // W_l = (1 - eta_w lambda) (W_l + eta_w D_l^T M_l) as one grouped GEMM over
+    // the batch (K = rows; D_l and M_l transposed so K is contiguous), the
+    // bias sums, then the transposed copy W_l^T that the update phase reads.
+    const int kp = (int)round_up((size_t)batch, kFeatPad);
+    std::vector<void*> tmp;
+    std::vector<ProblemSet> sets;
+    const Tile tile = Tile{64, 64};
+    for (int l = 1; l < L && !st; ++l) {
+        const int lo = m->s[l - 1], sz = m->s[l];
+        const int Rlo = (int)round_up(lo, kRowPad), Rsz = (int)round_up(sz, kRowPad);
+        void *dt = nullptr, *mt = nullptr;
+        if ((st = pool_alloc(&dt, (size_t)Rlo * kp * 4, s))) break;
+        tmp.push_back(dt);
+        if ((st = pool_alloc(&mt, (size_t)Rsz * kp * 4, s))) break;
+        tmp.push_back(mt);
+        const int g1 = (int)std::min<size_t>(((size_t)Rlo * kp + 255) / 256, 8192);
+        const int g2 = (int)std::min<size_t>(((size_t)Rsz * kp + 255) / 256, 8192);
+        hipLaunchKernelGGL(pack_kernel<float>, dim3(g1), dim3(256), 0, s, (const void*)w->D[l], 1, m->P[l - 1], batch,
+                           1, dt, Rlo, kp, kp);
+        hipLaunchKernelGGL(pack_kernel<float>, dim3(g2), dim3(256), 0, s, (const void*)w->M[l], 1, m->P[l], batch, 1,
+                           mt, Rsz, kp, kp);
+        if ((st = from_hip(hipGetLastError(), "pack_kernel launch"))) break;
+        const int gb = std::min((lo + 255) / 256, 1024);
+        hipLaunchKernelGGL(bias_update_kernel, dim3(gb), dim3(256), 0, s, (const float*)w->D[l], m->P[l - 1], batch,
+                           lo, m->bias[l], eta_w);
+        if ((st = from_hip(hipGetLastError(), "bias_update_kernel launch"))) break;
+        if (sets.empty() || sets.back().n == kMaxProblems) {
+            sets.emplace_back();
+            std::memset(&sets.back(), 0, sizeof(ProblemSet));
+        }
+        Problem& p = sets.back().p[sets.back().n++];
+        p.A = dt;
+        p.lda = kp;
+        p.B = mt;
+        p.ldb = kp;
+        p.M = lo;
+        p.N = sz;
+        p.K = kp;
+        p.tiles_m = (lo + tile.m - 1) / tile.m;
+        p.tiles_n = (sz + tile.n - 1) / tile.n;
+        p.tiles = p.tiles_m * p.tiles_n;
+        p.ldo = m->P[l];
+        p.m = (float*)m->W[l];
+    }
+    if (!st) {
+        const float keep = 1.f - eta_w * weight_decay;
+        PhaseArgs a;
+        std::memset(&a, 0, sizeof a);
+        a.alpha = eta_w * keep;
+        a.beta = keep;
+        a.tile_order = m->tile_order;
+        for (auto& ps : sets)
+            if ((st = launch_phase(PCD_F32, tile, EPI_PLAIN, ps, a, s))) break;
+    }
+    for (int l = 1; l < L && !st; ++l) {
+        const int lo = m->s[l - 1], sz = m->s[l];
+        const int Rsz = (int)round_up(sz, kRowPad);
+        const int g = (int)std::min<size_t>(((size_t)Rsz * m->P[l - 1] + 255) / 256, 8192);
+        hipLaunchKernelGGL(pack_kernel<float>, dim3(g), dim3(256), 0, s, (const void*)m->W[l], 1, m->P[l], lo, 1,
+                           m->WT[l], Rsz, m->P[l - 1], m->P[l - 1]);
+        st = from_hip(hipGetLastError(), "pack_kernel launch (W^T)");
+    }
+    for (void* t : tmp) {
+        int st2 = pool_free(t, s);
+        if (!st) st = st2;
+    }
+    if (scratch) {
+        int st2 = pool_free(scratch, s);
+        if (!st) st = st2;
+    }
+    return st;
+}
+
+int pcd_pc_model_get_weights(pcd_model* m, int layer, float* W_out, float* b_out) {
+    if (int st = check_model(m)) return st;
+    if (layer < 1 || layer >= m->L) return fail(PCD_INVALID_VALUE, "layer %d is not in 1..%d", layer, m->L - 1);
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(hipDeviceSynchronize());
+    const int lo = m->s[layer - 1], sz = m->s[layer];
+    if (W_out) {
+        if (m->dtype == PCD_F32) {
+            HIP_TRY(hipMemcpy2D(W_out, (size_t)sz * 4, m->W[layer], (size_t)m->P[layer] * 4, (size_t)sz * 4, lo,
+                                hipMemcpyDeviceToHost));
+        } else {
+            std::vector<uint16_t> bits((size_t)lo * sz);
+            HIP_TRY(hipMemcpy2D(bits.data(), (size_t)sz * 2, m->W[layer], (size_t)m->P[layer] * 2, (size_t)sz * 2, lo,
+                                hipMemcpyDeviceToHost));
+            for (size_t i = 0; i < bits.size(); ++i) {
+                if (m->dtype == PCD_BF16) {
+                    const uint32_t u = (uint32_t)bits[i] << 16;
+                    std::memcpy(&W_out[i], &u, 4);
+                } else {
+                    _Float16 h;
+                    std::memcpy(&h, &bits[i], 2);
+                    W_out[i] = (float)h;
+                }
+            }
+        }
+    }
+    if (b_out) HIP_TRY(hipMemcpy(b_out, m->bias[layer], (size_t)lo * 4, hipMemcpyDeviceToHost));
+    return PCD_SUCCESS;
 }
 
 }  // extern "C"

@@ -26,7 +26,12 @@ def _act(name):
     }[name]
 
 
-def autograd_relax(sizes, act, eta, W, b, prec, x0, steps, act_reg=0.0, ffg=False):
+def autograd_relax(sizes, act, eta, W, b, prec, x0, steps, act_reg=0.0, ffg=False, top_clamp=None,
+                   want_delta=False):
+    """Settles from zero hidden states; with top_clamp [B, s_top] the top layer
+    is held there (not a free variable).  With want_delta it also returns, for
+    every layer l >= 1, delta_l = -dF/dpre_l at the last step's pre-update
+    state (autograd through the pre-activation itself)."""
     f = _act(act)
     L = len(sizes)
     dt = torch.float64
@@ -36,23 +41,59 @@ def autograd_relax(sizes, act, eta, W, b, prec, x0, steps, act_reg=0.0, ffg=Fals
     x = torch.tensor(np.asarray(x0, dtype=np.float64), dtype=dt)
     B = x.shape[0]
     mu = [x] + [torch.zeros(B, s, dtype=dt) for s in sizes[1:]]
+    nfree = L - 1
+    if top_clamp is not None:
+        mu[-1] = torch.tensor(np.asarray(top_clamp, dtype=np.float64), dtype=dt).reshape(B, sizes[-1])
+        nfree = L - 2
     if ffg:
         for l in range(L - 1, 0, -1):
             pred = f(mu[l] @ Wt[l - 1].T + bt[l - 1])
             if l > 1:
                 mu[l - 1] = pred.detach().clone()
     energies = np.zeros((steps, B))
+    deltas = None
     for t in range(steps):
-        free = [m.clone().requires_grad_(True) for m in mu[1:]]
-        full = [mu[0]] + free
+        free = [m.clone().requires_grad_(True) for m in mu[1:1 + nfree]]
+        full = [mu[0]] + free + mu[1 + nfree:]
         Fb = torch.zeros(B, dtype=dt)
+        pres = []
         for l in range(L - 1):
-            r = full[l] - f(full[l + 1] @ Wt[l].T + bt[l])
+            pre = full[l + 1] @ Wt[l].T + bt[l]
+            if want_delta and t == steps - 1:
+                if pre.requires_grad:
+                    pre.retain_grad()
+                else:   # the clamped top's pre-activation: a leaf of its own
+                    pre = pre.detach().requires_grad_(True)
+            pres.append(pre)
+            r = full[l] - f(pre)
             Fb = Fb + 0.5 * P[l] * (r * r).sum(dim=1)
         energies[t] = Fb.detach().numpy()
         F = Fb.sum()
         if act_reg > 0:
             F = F + act_reg * sum(m.abs().sum() for m in free)
-        grads = torch.autograd.grad(F, free)
-        mu = [mu[0]] + [(m - eta * g).detach() for m, g in zip(free, grads)]
+        if want_delta and t == steps - 1:
+            F.backward()
+            grads = [m.grad for m in free]
+            deltas = [None] + [(-p.grad).numpy() for p in pres]
+        else:
+            grads = torch.autograd.grad(F, free) if free else []
+        mu = [mu[0]] + [(m - eta * g).detach() for m, g in zip(free, grads)] + mu[1 + nfree:]
+    if want_delta:
+        return mu[-1].numpy(), [m.numpy() for m in mu], energies, deltas
     return mu[-1].numpy(), [m.numpy() for m in mu], energies
+
+
+def autograd_learn(sizes, act, eta, W, b, prec, x0, labels, steps, eta_w, weight_decay=0.0):
+    """Learning step from the autograd settling: W_l += eta_w delta_l^T mu_l
+    (settled mu_l), b_l += eta_w sum delta_l, then W_l -= eta_w lambda W_l."""
+    _, mus, energies, deltas = autograd_relax(sizes, act, eta, W, b, prec, x0, steps, top_clamp=labels,
+                                              want_delta=True)
+    new_w, new_b = [], []
+    for l in range(1, len(sizes)):
+        w = np.asarray(W[l - 1], dtype=np.float64) + eta_w * deltas[l].T @ mus[l]
+        bb = np.asarray(b[l - 1], dtype=np.float64) + eta_w * deltas[l].sum(axis=0)
+        if weight_decay > 0:
+            w = w - eta_w * weight_decay * w
+        new_w.append(w)
+        new_b.append(bb)
+    return new_w, new_b, energies[-1]

@@ -86,3 +86,12 @@ def test_no_device_reported_without_gpu():
     n = ctypes.c_int(-1)
     assert _native.lib().pcd_get_device_count(ctypes.byref(n)) == DeviceStatus.NoDevice
     assert n.value == 0
+
+
+def test_clamped_classify_learn_argument_errors_without_gpu():
+    # null model handle first (NotInitialized), before any device work
+    L = _native.lib()
+    assert L.pcd_pc_relax_clamped(None, None, None, 1, 1, None, None, None) == DeviceStatus.NotInitialized
+    assert L.pcd_pc_classify(None, None, 1, 1, None, None, None, None) == DeviceStatus.NotInitialized
+    assert L.pcd_pc_learn(None, None, None, 1, 1, 0.01, 0.0, None, None) == DeviceStatus.NotInitialized
+    assert L.pcd_pc_model_get_weights(None, 1, None, None) == DeviceStatus.NotInitialized
