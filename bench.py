@@ -14,6 +14,11 @@ Workloads:
       batch log-uniform in [1,512] and T uniform in [8,64] (seeded), early exit
       when energy/sample < 1e-3; one pass = one packed pcd_pc_relax_ragged call,
       value = sum over requests of rows x steps actually run / elapsed.
+  c1cls    c1's network classifying a batch of 64 by minimum energy
+           (Network.PredictCore per sample: 10 settlings with the top clamped
+           to each one-hot label); value counts the 640 settled rows x T.
+  c1learn  c1's network taking a learning step (Network.Learn) on a batch of
+           64 labelled samples; value counts 64 rows x T.
 
 The JSON line carries the roofline of the dominant kernel (average duration
 of its launches from HIP events on the library's stream) and a CPU baseline:
@@ -45,6 +50,13 @@ CONFIGS = {
     # Xavier-normal, the reference's tanh initialiser
     "c4": dict(sizes=[2048] * 4, act=1, dtype="f32", eta=0.1, x="normal", init="xavier", requests=64,
                bmax=512, tmin=8, tmax=64, exit_rule="absolute", exit_thr=1e-3, seed=4),
+    # c1's network used the way the reference's Trainer does: minimum-energy
+    # classification of a batch (Network.PredictCore per sample, 10 clamped
+    # settlings each) and the learning step (Network.Learn) on a batch
+    "c1cls": dict(sizes=[784, 256, 256, 10], act=1, dtype="f32", batch=64, T=20, eta=0.1, x="uniform01",
+                  init="xavier", mode="classify"),
+    "c1learn": dict(sizes=[784, 256, 256, 10], act=1, dtype="f32", batch=64, T=20, eta=0.1, x="uniform01",
+                    init="xavier", mode="learn", eta_w=0.01),
 }
 ACT_NAME = {1: "tanh", 4: "gelu"}
 
@@ -285,6 +297,117 @@ def bench_ragged(args, cfg):
     model.close()
 
 
+def bench_clamped(args, cfg):
+    """c1cls / c1learn: one pass = one pcd_pc_classify (every sample settled
+    against every class) or one pcd_pc_learn over the batch."""
+    import torch
+    from predicitivecoding_amd import GenerativeSnapshot, PcDeviceModel
+    sizes, B, T, mode = cfg["sizes"], cfg["batch"], cfg["T"], cfg["mode"]
+    C = sizes[-1]
+    rows = B * C if mode == "classify" else B
+    print(f"# bench {args.config}: {mode} sizes={sizes} B={B} T={T} rows={rows}", file=sys.stderr, flush=True)
+    W, b = make_weights(cfg)
+    snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
+    model = PcDeviceModel(snap, cfg["dtype"])
+    if args.tile_order >= 0:
+        model.set_option("tile_order", args.tile_order)
+    if args.tile:
+        model.set_option("tile", args.tile)
+    x = make_inputs(cfg)
+    labels = torch.zeros((B, C), device="cuda", dtype=torch.float32)
+    labels[torch.arange(B, device="cuda"), torch.arange(B, device="cuda") % C] = 1.0
+    ce = torch.empty((B, C), device="cuda", dtype=torch.float32)
+    cls = torch.empty((B,), device="cuda", dtype=torch.int32)
+    be = torch.empty((B,), device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+
+    def one_pass():
+        if mode == "classify":
+            model.classify_device(x.data_ptr(), B, T, ce.data_ptr(), cls.data_ptr(), be.data_ptr())
+        else:
+            model.learn_device(x.data_ptr(), labels.data_ptr(), B, T, cfg["eta_w"], 0.0, be.data_ptr())
+
+    for _ in range(args.warmup):
+        one_pass()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_pass()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = rows * T * args.steps / elapsed
+    print(f"# timed {args.steps} passes: {ms_per_step:.3f} ms/pass, {value:.4g} sample-steps/s "
+          f"({B * args.steps / elapsed:.4g} samples/s)", file=sys.stderr, flush=True)
+
+    model.set_option("profile", 1)
+    one_pass()
+    torch.cuda.synchronize()
+    err_ms, upd_ms, launches = model.profile_result()
+    model.set_option("profile", 0)
+    S = sum(sizes[l] * sizes[l - 1] for l in range(1, len(sizes)))
+    S_free = S - sizes[-1] * sizes[-2]                 # the clamped top layer is never updated
+    flops = {"error_phase": 2.0 * rows * S, "update_phase": 2.0 * rows * S_free}
+    ms = {"error_phase": err_ms, "update_phase": upd_ms}
+    dom_name = max(ms, key=ms.get)
+    achieved = flops[dom_name] / (ms[dom_name] * 1e-3)
+    peak = PEAK[cfg["dtype"]]
+    roofline = {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / peak, "traffic": traffic_from_profiles(args.config, dom_name), "kernel": dom_name,
+                "kernel_ms": ms[dom_name], "error_phase_ms": err_ms, "update_phase_ms": upd_ms,
+                "flop_per_launch": flops[dom_name], "launches_timed": launches,
+                "path_frac": (2.0 * (S + S_free) * value) / peak}
+    print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch; {dom_name} at "
+          f"{achieved / 1e12:.1f} TFLOP/s = {100 * achieved / peak:.1f}% of peak", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_clamped(cfg, W, b, x.cpu().numpy(), labels.cpu().numpy(), args.cpu_budget)
+        print(f"# cpu baseline: {cpu['value']:.4g} sample-steps/s on {cpu['cores']} threads", file=sys.stderr,
+              flush=True)
+    what = ("minimum-energy classification, every sample settled against each of the "
+            f"{C} one-hot labels" if mode == "classify" else f"learning step, eta_w={cfg['eta_w']}")
+    rec = {
+        "metric": "relaxed samples*steps/sec at 1 GPU and % of MFMA/HBM roofline",
+        "value": value, "unit": "sample-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": cfg["dtype"], "data": "synthetic (seeded random weights and inputs)",
+        "config": {"workload": f"{args.config}: {'-'.join(map(str, sizes))} tanh f32, B={B}, T={T}, "
+                               f"eta={cfg['eta']}: {what}",
+                   "batch": B, "relaxed_rows": rows, "relax_steps": T, "layer_sizes": sizes,
+                   "samples_per_s": B * args.steps / elapsed, "parallelism": "single GPU"},
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec))
+    model.close()
+
+
+def cpu_baseline_clamped(cfg, W, b, x_host, labels_host, budget_s=10.0):
+    """The oracle's per-sample PredictCore / Learn loop (one sample at a time,
+    as Trainer.Evaluate / TrainEpoch call them), on the first samples of the
+    batch until the budget is spent."""
+    from oracle import pc_oracle
+    pc_oracle.set_threads(1)
+    sizes, act, T = cfg["sizes"], ACT_NAME[cfg["act"]], cfg["T"]
+    P = [1.0] * len(sizes)
+    C = sizes[-1]
+    per_sample_rows = C if cfg["mode"] == "classify" else 1
+    done, t0 = 0, time.perf_counter()
+    Wc, bc = W, b
+    while done < cfg["batch"] and (time.perf_counter() - t0) < budget_s:
+        if cfg["mode"] == "classify":
+            pc_oracle.classify(sizes, act, cfg["eta"], W, b, P, x_host[done:done + 1], T)
+        else:
+            Wc, bc, _ = pc_oracle.learn(sizes, act, cfg["eta"], Wc, bc, P, x_host[done:done + 1],
+                                        labels_host[done:done + 1], T, cfg["eta_w"])
+        done += 1
+    dt = time.perf_counter() - t0
+    name = "Network.PredictCore" if cfg["mode"] == "classify" else "Network.Learn"
+    return {"value": done * per_sample_rows * T / dt, "unit": "sample-steps/s", "cores": 1, "kind": "port",
+            "sample": f"oracle {name} one sample at a time (batch-1 settlings), {done} of {cfg['batch']} samples "
+                      f"x {per_sample_rows} settlings x {T} steps, {dt:.1f} s"}
+
+
 def cpu_baseline_ragged(cfg, W, b, x_host, offsets, steps, budget_s=10.0):
     """The oracle's per-request relaxation with the same exit rule, on the
     first requests that fit the time budget."""
@@ -351,6 +474,9 @@ def main():
     cfg = CONFIGS[args.config]
     if args.config == "c4":
         bench_ragged(args, cfg)
+        return
+    if "mode" in cfg:
+        bench_clamped(args, cfg)
         return
     sizes, B, T = cfg["sizes"], cfg["batch"], cfg["T"]
     print(f"# bench {args.config}: sizes={sizes} B={B} T={T} dtype={cfg['dtype']}", file=sys.stderr, flush=True)
