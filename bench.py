@@ -61,6 +61,12 @@ CONFIGS = {
 ACT_NAME = {1: "tanh", 4: "gelu"}
 
 
+def apply_options(model, args):
+    for item in args.option:
+        name, _, value = item.partition("=")
+        model.set_option(name, int(value))
+
+
 def flops_per_sample_step(sizes):
     return 4.0 * sum(sizes[l] * sizes[l - 1] for l in range(1, len(sizes)))
 
@@ -228,6 +234,7 @@ def bench_ragged(args, cfg):
     W, b = make_weights(cfg)
     snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
     model = PcDeviceModel(snap, cfg["dtype"])
+    apply_options(model, args)
     if args.tile_order >= 0:
         model.set_option("tile_order", args.tile_order)
     g = torch.Generator(device="cuda").manual_seed(1)
@@ -309,6 +316,7 @@ def bench_clamped(args, cfg):
     W, b = make_weights(cfg)
     snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
     model = PcDeviceModel(snap, cfg["dtype"])
+    apply_options(model, args)
     if args.tile_order >= 0:
         model.set_option("tile_order", args.tile_order)
     if args.tile:
@@ -450,6 +458,8 @@ def main():
     ap.add_argument("--tile", type=int, default=0, help="force the GEMM tile rows (and columns unless --tile-n)")
     ap.add_argument("--tile-n", type=int, default=0)
     ap.add_argument("--tile-order", type=int, default=-1, help="force the tile order option (0 interleaved, 1 contiguous)")
+    ap.add_argument("--option", action="append", default=[], metavar="NAME=VALUE",
+                    help="set a pcd_pc_set_option relaxation option (repeatable), e.g. split_k=0")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the copy kernel that calibrates FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "CALIB_FETCH_DIR", "CALIB_WRITE_DIR"),
@@ -483,6 +493,7 @@ def main():
     W, b = make_weights(cfg)
     snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
     model = PcDeviceModel(snap, cfg["dtype"])
+    apply_options(model, args)
     if args.tile_order >= 0:
         model.set_option("tile_order", args.tile_order)
     if args.tile:

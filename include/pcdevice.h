@@ -262,6 +262,8 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *   tile, tile_n force a GEMM tile (0 = automatic choice)
  *   tile_order   0: every XCD runs an eighth of each problem's tiles (default);
  *                1: every XCD runs one contiguous eighth of the phase's tiles
+ *   split_k      1: phases with fewer tiles than half the CUs split K over
+ *                several workgroups per tile (default); 0: never
  *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
  *                time every phase launch with HIP events (pcd_pc_profile_result) */
 int pcd_pc_set_option(pcd_model* model, const char* name, int value);

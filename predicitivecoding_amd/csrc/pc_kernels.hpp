@@ -91,7 +91,8 @@ struct Problem {
     const void* B;        // [>= tiles_n*BN rows x ldb], K-contiguous
     int lda, ldb;         // leading dimensions, elements
     int M, N, K;          // valid rows, valid columns, K (a multiple of the stage depth)
-    int tiles_m, tiles_n, tiles;   // tile grid of the output, tiles = tiles_m * tiles_n
+    int tiles_m, tiles_n;  // tile grid of the output
+    int tiles;            // work units: tiles_m * tiles_n * ksplit
     int ldo;              // leading dimension of every [rows x N] epilogue operand
     const float* bias;    // ERROR/FFG: b_l [N]
     const float* mlow;    // ERROR: fp32 state M_{l-1}
@@ -102,7 +103,14 @@ struct Problem {
     const float* eself;   // UPDATE: X_l from the error phase (nullable for the top layer)
     float prec;           // ERROR: P_{l-1}
     int slot_base;        // ERROR: first energy partial slot of this problem
+    int ksplit;           // K ranges per tile (<= 1: none); the last range to finish runs the epilogue
+    int ksplit_pad;
+    float* part;          // split-K: fp32 partial tiles [tiles_m * tiles_n * ksplit x BM * BN]
+    int* count;           // split-K: finished ranges per tile [tiles_m * tiles_n], zero between launches
 };
+
+// Most K ranges a split-K tile is cut into.
+constexpr int kMaxSplit = 8;
 
 // Problems of one grouped launch, passed by value in the kernel arguments.
 constexpr int kMaxProblems = 16;
@@ -381,6 +389,11 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     }
     if (local < 0) return;  // a spare workgroup of this XCD (the grid is 8 x the largest XCD share)
     const Problem P = load_problem(kprobs + p);
+    // Split-K: unit `local` is K range `split` of tile `local / ksplit` (a
+    // tile's ranges are consecutive units, so they run on one XCD).
+    const int ks = P.ksplit > 1 ? P.ksplit : 1;
+    const int split = local % ks;
+    local /= ks;
     // Grouped order: runs of 8 row tiles share one column tile.
     const int G = 8;
     int group = local / (G * P.tiles_n);
@@ -421,11 +434,13 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
 #pragma unroll
             for (int j = 0; j < C::FN; ++j) accs[k][i][j] = f32x16{};
 
-    const char* Ag = (const char*)P.A + (size_t)row0 * P.lda * OPB;
-    const char* Bg = (const char*)P.B + (size_t)col0 * P.ldb * OPB;
-    const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
     constexpr int KE = C::RB / OPB;  // K elements per stage
-    const int nk = P.K / KE;
+    const int nk_all = P.K / KE;
+    const int kb = split * nk_all / ks;             // this unit's stages [kb, kb + nk)
+    const int nk = (split + 1) * nk_all / ks - kb;
+    const char* Ag = (const char*)P.A + (size_t)row0 * P.lda * OPB + (size_t)kb * C::RB;
+    const char* Bg = (const char*)P.B + (size_t)col0 * P.ldb * OPB + (size_t)kb * C::RB;
+    const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
 
     // This lane's source of each of its wave's QPW loads per stage: combined
     // stage row R = q*ROWS_PER_LOAD + lane/UNITS (A rows, then B rows),
@@ -548,6 +563,92 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
             for (int j = 0; j < C::FN; ++j) accs[0][i][j] += accs[decltype(Kc)::value][i][j];
     });
     f32x16 (&acc)[C::FM][C::FN] = accs[0];
+
+    // ---- split-K: publish this range's partial tile; the range that finishes
+    // last sums all of them in range order (the same sum whichever finishes
+    // last) and goes on to the epilogue, the others are done.
+    // The partials move with device-scope (sc1) stores and loads, which the
+    // XCDs' L2s do not hold non-coherently: a range's stores have reached the
+    // device's coherence point once vmcnt drains, before its count increment,
+    // and the last range reads them back from that point.  No L2 write-back
+    // or invalidate (what a device-scope fence costs) touches the other
+    // workgroups' cached operands.
+    if (ks > 1) {
+        const int tile = local;
+        // Lane-contiguous layout: block (i, j) of this wave holds each lane's 16
+        // accumulators as 8 consecutive 64-bit pairs (a wave's block is 4 KB).
+        typedef unsigned long long u64;
+        u64* part = (u64*)(P.part + (size_t)tile * ks * (BM * BN));
+        auto slot_of = [&](int i, int j) PCD_INLINE { return (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 8; };
+        constexpr int UNIT = BM * BN / 2;   // 64-bit words of one partial tile
+        u64* mine = part + (size_t)split * UNIT;
+        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+            static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                constexpr int i = decltype(I)::value, j = decltype(J)::value;
+                static_for<0, 8>([&](auto Q) PCD_INLINE {
+                    constexpr int q = decltype(Q)::value;
+                    const u64 w = (u64)__float_as_uint(acc[i][j][2 * q]) | ((u64)__float_as_uint(acc[i][j][2 * q + 1]) << 32);
+                    __hip_atomic_store(mine + slot_of(i, j) + q, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                });
+            });
+        });
+        wait_vmcnt<0>();      // this lane's partial stores are complete
+        __syncthreads();      // ... every lane's; the stage ring is no longer read
+        int* flag = (int*)smem;
+        if (tid == 0)
+            *flag = __hip_atomic_fetch_add(P.count + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const bool last = *flag == ks - 1;
+        if (!last) return;
+        if (tid == 0) __hip_atomic_store(P.count + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+        // Per block, four ranges at a time: their words are all requested
+        // before any is summed (two round trips for eight ranges), and the sum
+        // runs over the ranges in order.
+        constexpr int KG = 4;
+        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+            static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                constexpr int i = decltype(I)::value, j = decltype(J)::value;
+                float lo[8], hi[8];
+                static_for<0, kMaxSplit / KG>([&](auto Gc) PCD_INLINE {
+                    constexpr int g = decltype(Gc)::value;
+                    if (g * KG < ks) {
+                        u64 pv[KG][8];
+                        static_for<0, KG>([&](auto K) PCD_INLINE {
+                            constexpr int k = g * KG + decltype(K)::value;
+                            if (k < ks && k != split)
+                                static_for<0, 8>([&](auto Q) PCD_INLINE {
+                                    pv[decltype(K)::value][decltype(Q)::value] =
+                                        __hip_atomic_load(part + (size_t)k * UNIT + slot_of(i, j) + decltype(Q)::value,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                });
+                        });
+                        static_for<0, 8>([&](auto Q) PCD_INLINE {
+                            constexpr int q = decltype(Q)::value;
+                            static_for<0, KG>([&](auto K) PCD_INLINE {
+                                constexpr int k = g * KG + decltype(K)::value;
+                                if (k < ks) {
+                                    float a, b;
+                                    if (k == split) {
+                                        a = acc[i][j][2 * q];
+                                        b = acc[i][j][2 * q + 1];
+                                    } else {
+                                        a = __uint_as_float((uint32_t)pv[decltype(K)::value][q]);
+                                        b = __uint_as_float((uint32_t)(pv[decltype(K)::value][q] >> 32));
+                                    }
+                                    lo[q] = k == 0 ? a : lo[q] + a;
+                                    hi[q] = k == 0 ? b : hi[q] + b;
+                                }
+                            });
+                        });
+                    }
+                });
+                static_for<0, 8>([&](auto Q) PCD_INLINE {
+                    acc[i][j][2 * decltype(Q)::value] = lo[decltype(Q)::value];
+                    acc[i][j][2 * decltype(Q)::value + 1] = hi[decltype(Q)::value];
+                });
+            });
+        });
+    }
 
     // ---- epilogue
     // Row of register r of a block in row-block i: 8*(r/4) + 4*half + r%4.

@@ -228,6 +228,8 @@ struct Workspace {
     std::vector<float*> E;             // [L] X_l = M_l - eta (E_l + lambda sign M_l), 1 <= l <= L-2, fp32 [cap x P_l]
     float* energy_part = nullptr;      // [slots x cap]
     int slots_cap = 0;
+    float* split_part = nullptr;       // split-K partial tiles, kSplitPartTiles x 128 x 128 fp32
+    int* split_count = nullptr;        // split-K finished-range counters, zero between launches
     hipStream_t capture = nullptr;     // private stream used for graph capture
     std::vector<std::unique_ptr<Plan>> plans;
     std::vector<void*> owned;          // every hipMalloc'ed buffer
@@ -257,7 +259,7 @@ struct pcd_model {
     std::mutex mu;
     std::vector<std::unique_ptr<Workspace>> ws;
     // options
-    int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED;
+    int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED, split_k = 1;
     float prof_err_ms = 0.f, prof_upd_ms = 0.f;
     int prof_launches = 0;
     uint64_t clock = 0;
@@ -334,6 +336,67 @@ int max_energy_slots(const pcd_model* m) {
     return slots;
 }
 
+// Split-K.  A phase whose output tiles leave CUs idle (at most half as many
+// tiles as CUs, tiles of at most 128 x 128) cuts each tile's K into up to
+// cus / tiles (<= kMaxSplit) ranges of at least kSplitMinStages stages; the partial tiles
+// go to workspace scratch and the range that finishes last reduces them and
+// runs the epilogue.  Units of a phase never exceed the CU count, so the
+// scratch holds `cus` partial tiles of 128 x 128 and as many counters.
+int split_part_tiles(const pcd_model* m) { return std::max(m->cus, 1); }
+
+// Fewest K stages a split-K range runs: a range also pays its partial tile's
+// store, the count and (last range) the reduction, a few microseconds.
+#ifndef PCD_SPLIT_MIN_STAGES
+#define PCD_SPLIT_MIN_STAGES 12
+#endif
+constexpr int kSplitMinStages = PCD_SPLIT_MIN_STAGES;
+
+int split_factor(const pcd_model* m, long tiles, Tile tile) {
+    if (!m->split_k || tile.m * tile.n > 128 * 128 || tiles < 1 || tiles * 2 > m->cus) return 1;
+    return (int)std::min<long>(kMaxSplit, m->cus / tiles);
+}
+
+// K elements of one LDS stage of `tile` for the model's operand type.
+int stage_k(const pcd_model* m, Tile tile) {
+    int rb = 64;
+    if (tile.m == 128 && tile.n == 128) rb = TileCfg<128, 128>::RB;
+    else if (tile.m == 256 && tile.n == 256) rb = TileCfg<256, 256>::RB;
+    return rb / op_bytes(m->dtype);
+}
+
+// Gives every problem of a phase its split factor and its share of the scratch.
+// Besides the few-tiles split of the whole phase, a problem whose eighth (one
+// XCD's share) has fewer tiles than the XCD has CUs is split to about one unit
+// per CU: its tiles would otherwise give a part of the CUs one more whole tile
+// than the rest (c2's update phase: 8 tiles of the 256-wide layer per XCD of 32
+// CUs next to 3 x 32 full tiles).  Splitting stops where the scratch is spent.
+void assign_split(const pcd_model* m, const Workspace* w, Tile tile, std::vector<ProblemSet>& sets) {
+    long tiles = 0;
+    for (auto& ps : sets)
+        for (int i = 0; i < ps.n; ++i) tiles += (long)ps.p[i].tiles_m * ps.p[i].tiles_n;
+    const int f = split_factor(m, tiles, tile);
+    const int per_xcd = std::max(1, m->cus / kXcds);
+    const bool small_tile = tile.m * tile.n <= 128 * 128;
+    long units = 0, counters = 0;
+    for (auto& ps : sets)
+        for (int i = 0; i < ps.n; ++i) {
+            Problem& p = ps.p[i];
+            const int t = p.tiles_m * p.tiles_n;
+            const int share = (t + kXcds - 1) / kXcds;
+            const int fb = (m->split_k && small_tile && share < per_xcd) ? per_xcd / share : 1;
+            int ks = std::max(1, std::min({std::max(f, fb), kMaxSplit, p.K / stage_k(m, tile) / kSplitMinStages}));
+            if (ks > 1 && units + (long)t * ks > split_part_tiles(m)) ks = 1;
+            p.ksplit = ks;
+            p.tiles = t * ks;
+            if (ks > 1) {
+                p.part = w->split_part + units * (long)tile.m * tile.n;
+                p.count = w->split_count + counters;
+                units += (long)t * ks;
+                counters += t;
+            }
+        }
+}
+
 int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out) {
     Workspace* w = nullptr;
     for (auto& x : m->ws)
@@ -369,6 +432,9 @@ int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out
     }
     w->slots_cap = slots;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->energy_part, (size_t)slots * need * 4))) return st;
+    if ((st = dev_alloc_zero(w->owned, (void**)&w->split_part, (size_t)split_part_tiles(m) * 128 * 128 * 4)))
+        return st;
+    if ((st = dev_alloc_zero(w->owned, (void**)&w->split_count, (size_t)split_part_tiles(m) * 4))) return st;
     HIP_TRY(hipStreamCreateWithFlags(&w->capture, hipStreamNonBlocking));
     *out = w;
     return PCD_SUCCESS;
@@ -434,6 +500,8 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         p.mop = m->dtype == PCD_F32 ? nullptr : w->S[l];
         p.eself = l <= L - 2 ? w->E[l] : nullptr;
     }
+    assign_split(m, w, tile, err);
+    assign_split(m, w, tile, upd);
     *nslots = slot;
 }
 
@@ -1074,6 +1142,7 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
             return fail(PCD_INVALID_VALUE, "tile_n: unsupported tile %d x %d (set tile first)", m->tile_m, value);
         m->tile_n = value;
     } else if (n == "profile") m->profile = value ? 1 : 0;
+    else if (n == "split_k") m->split_k = value ? 1 : 0;
     else if (n == "tile_order") {
         if (value != TILE_INTERLEAVED && value != TILE_CONTIGUOUS)
             return fail(PCD_INVALID_VALUE, "tile_order must be 0 (interleaved) or 1 (contiguous)");
