@@ -165,7 +165,9 @@ int pcd_gemm_f16(const uint16_t* dA, const uint16_t* dB, float* dC, int m, int k
  *   ffg                 UseFeedforwardGistInit
  *   dtype               enum pcd_dtype
  * The library keeps its own device copies (W and W^T in the operand dtype,
- * biases in fp32); host memory is read during the call only. */
+ * biases in fp32); host memory is read during the call only.  W and b may
+ * both be null: the weights and biases then start at zero, for
+ * pcd_pc_model_load_record to fill. */
 int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta, float act_reg, int ffg,
                         const float* const* W, const float* const* b, const float* precisions,
                         int dtype, pcd_model** out);
@@ -252,6 +254,21 @@ int pcd_pc_learn(pcd_model* model, const float* x0, const float* labels, int bat
  *   b_out  nullable host [sizes[layer-1]]
  * Waits for the device. */
 int pcd_pc_model_get_weights(pcd_model* model, int layer, float* W_out, float* b_out);
+
+/* Loads one LayerSerializer record (PredicitiveCoding/Model/LayerSerializer.cs:8-41,
+ * the layer's persisted bytes, host memory) into the model: layer `layer`'s
+ * precision and, for layer >= 1, its weights and bias, straight into the
+ * device operands in the record's own format:
+ *   float32, Half (flag 4), bfloat16 (flag 8): widened exactly, then stored in
+ *     the operand type (a record in the operand's own 16-bit format is copied
+ *     bit for bit);
+ *   int8 affine per row (flag 16): dequantized on the device as
+ *     (q - z) * s (ReadInt8Weights, :299-312).
+ * Deserialize's checks apply: sizes must match the model ("Layer size
+ * mismatch", :154-157); a record with a diagonal precision or a prior mean is
+ * PCD_NOT_SUPPORTED, as the generative snapshot refuses them
+ * (Network.cs:1334-1338).  Waits for the device. */
+int pcd_pc_model_load_record(pcd_model* model, int layer, const void* record, size_t bytes);
 
 /* Model properties (levels, sizes, dtype) for host wrappers. */
 int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_sizes, int* dtype);

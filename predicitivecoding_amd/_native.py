@@ -56,6 +56,7 @@ _SIGNATURES = {
     "pcd_pc_classify": [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p],
     "pcd_pc_learn": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_float, c_void_p, c_void_p],
     "pcd_pc_model_get_weights": [c_void_p, c_int, c_void_p, c_void_p],
+    "pcd_pc_model_load_record": [c_void_p, c_int, c_void_p, c_size_t],
     "pcd_pc_model_info": [c_void_p, P_int, P_int, c_int, P_int],
     "pcd_pc_set_option": [c_void_p, c_char_p, c_int],
     "pcd_pc_profile_result": [c_void_p, P_float, P_float, P_int],

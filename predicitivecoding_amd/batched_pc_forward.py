@@ -252,6 +252,37 @@ class PcDeviceModel:
                 t.free()
         return energy
 
+    def load_record(self, layer: int, record: bytes) -> None:
+        """pcd_pc_model_load_record: one LayerSerializer record (the layer's
+        persisted bytes) into the device operands."""
+        buf = ctypes.create_string_buffer(bytes(record), len(record))
+        call("pcd_pc_model_load_record", self.handle, int(layer), buf, len(record))
+
+    @classmethod
+    def from_records(cls, records, activation: int, eta: float, act_reg: float = 0.0, ffg: bool = False,
+                     dtype: str = "f32") -> "PcDeviceModel":
+        """A device model straight from the layers' records (layer 0 first), as
+        Network reopens its store: sizes and precisions from the record headers,
+        weights uploaded in their stored format."""
+        import struct
+        sizes = [struct.unpack_from("<i", r, 0)[0] for r in records]
+        precisions = [struct.unpack_from("<f", r, 8)[0] for r in records]
+        self = cls.__new__(cls)
+        self.snapshot = None
+        self.dtype = dtype
+        self.sizes = sizes
+        L = len(sizes)
+        if dtype not in DTYPE:
+            raise ArgumentException(f"dtype must be one of {sorted(DTYPE)}")
+        h = ctypes.c_void_p()
+        call("pcd_pc_model_create", (ctypes.c_int * L)(*sizes), L, int(activation), float(eta), float(act_reg),
+             int(bool(ffg)), None, None, (ctypes.c_float * L)(*precisions), DTYPE[dtype], ctypes.byref(h))
+        self.handle = h.value
+        self._finalizer = weakref.finalize(self, _native.lib().pcd_pc_model_destroy, self.handle)
+        for l, r in enumerate(records):
+            self.load_record(l, r)
+        return self
+
     def get_weights(self):
         """Current (W_l, b_l) of every layer l = 1..L-1 as host arrays."""
         W, b = [], []

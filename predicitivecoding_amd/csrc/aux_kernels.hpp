@@ -43,6 +43,38 @@ __global__ void pack_kernel(const void* __restrict__ src, int src_is_f32, int ro
     }
 }
 
+// Weight formats of a LayerSerializer record (Model/LayerSerializer.cs:19-36).
+enum RecordKind { REC_F32 = 0, REC_F16 = 1, REC_BF16 = 2, REC_I8 = 3 };
+
+// Pack the [rows x cols] weights of a record (optionally read transposed) into
+// a zero-padded [prow x pcol] operand buffer (row pitch pcol).  Values are
+// widened to fp32 as the reference's Deserialize does -- Half and bf16 exactly,
+// int8 as (q - z) * s with the row's scale and zero point (:299-312) -- and
+// then stored in the operand type, which keeps a record of the operand's own
+// 16-bit format bit for bit.
+template <typename OP>
+__global__ void pack_record_kernel(const void* __restrict__ src, int kind, const float* __restrict__ scales,
+                                   const int8_t* __restrict__ zeros, int rows, int cols, int trans,
+                                   void* __restrict__ dst, int prow, int pcol) {
+    const size_t n = (size_t)prow * pcol;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i / pcol), c = (int)(i % pcol);
+        float v = 0.f;
+        if (r < rows && c < cols) {
+            // logical (r, c) of op(W); W itself is [rows x cols], or [cols x rows] read transposed
+            const int pr = trans ? c : r, pc = trans ? r : c;
+            const size_t s = (size_t)pr * (trans ? rows : cols) + pc;
+            switch (kind) {
+            case REC_F32: v = ((const float*)src)[s]; break;
+            case REC_BF16: v = __uint_as_float((uint32_t)((const uint16_t*)src)[s] << 16); break;
+            case REC_F16: v = (float)__builtin_bit_cast(_Float16, ((const uint16_t*)src)[s]); break;
+            default: v = (float)((int)((const int8_t*)src)[s] - (int)zeros[pr]) * scales[pr]; break;
+            }
+        }
+        OpTraits<OP>::store(dst, i, v);
+    }
+}
+
 // Ragged early exit, one workgroup per request, between the error and the
 // update phase of step t: sums the request's row energies, records them and
 // decides whether step t is its last (Network.cs:895-905).

@@ -1025,7 +1025,8 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
                         pcd_model** out) {
     if (!out) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: null out pointer");
     *out = nullptr;
-    if (!sizes || !W || !b || !precisions) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: null pointer");
+    if (!sizes || !precisions) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: null pointer");
+    if (!W != !b) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: W and b must both be set or both be null");
     if (levels < 2) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: need at least 2 levels, got %d", levels);
     if (activation < PCD_ACT_LINEAR || activation > PCD_ACT_GELU)
         return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: unknown activation %d", activation);
@@ -1036,8 +1037,9 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
         if (sizes[l] < 1) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: sizes[%d] = %d", l, sizes[l]);
         if (!(precisions[l] > 0.f)) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: precision[%d] <= 0", l);
     }
-    for (int l = 1; l < levels; ++l)
-        if (!W[l - 1] || !b[l - 1]) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: null W/b for layer %d", l);
+    if (W)
+        for (int l = 1; l < levels; ++l)
+            if (!W[l - 1] || !b[l - 1]) return fail(PCD_INVALID_VALUE, "pcd_pc_model_create: null W/b for layer %d", l);
     int ndev = 0;
     if (int st = pcd_get_device_count(&ndev)) return st;
 
@@ -1067,8 +1069,15 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
         void *w = nullptr, *wt = nullptr, *bb = nullptr, *tmp = nullptr;
         if ((st = dev_alloc_zero(owned, &w, (size_t)Rlo * m->P[l] * ob)) ||
             (st = dev_alloc_zero(owned, &wt, (size_t)Rsz * m->P[l - 1] * ob)) ||
-            (st = dev_alloc_zero(owned, &bb, (size_t)m->P[l - 1] * 4)) ||
-            (st = dev_alloc_zero(owned, &tmp, (size_t)lo * sz * 4))) {
+            (st = dev_alloc_zero(owned, &bb, (size_t)m->P[l - 1] * 4))) {
+            cleanup();
+            return st;
+        }
+        m->W[l] = w;
+        m->WT[l] = wt;
+        m->bias[l] = (float*)bb;
+        if (!W) continue;   // zero weights, to be filled by pcd_pc_model_load_record
+        if ((st = dev_alloc_zero(owned, &tmp, (size_t)lo * sz * 4))) {
             cleanup();
             return st;
         }
@@ -1097,9 +1106,6 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
         if (e != hipSuccess) { cleanup(); return from_hip(e, "weight packing"); }
         (void)hipFree(tmp);
         owned.pop_back();
-        m->W[l] = w;
-        m->WT[l] = wt;
-        m->bias[l] = (float*)bb;
     }
     *out = m.release();
     return PCD_SUCCESS;
@@ -1514,5 +1520,122 @@ int pcd_pc_model_get_weights(pcd_model* m, int layer, float* W_out, float* b_out
     if (b_out) HIP_TRY(hipMemcpy(b_out, m->bias[layer], (size_t)lo * 4, hipMemcpyDeviceToHost));
     return PCD_SUCCESS;
 }
+
+// ------------------------------------------------------------ weight records
+
+// A LayerSerializer record (Model/LayerSerializer.cs:8-41): its header and
+// where its weights and bias sit.  Mu, PredictionError, PreActivation and
+// Prediction are a settling's state, which the device path makes itself.
+struct LayerRecord {
+    int size = 0, lower = 0, flags = 0, kind = REC_F32;
+    float precision = 0.f;
+    const uint8_t* weights = nullptr;   // payload in the stored format
+    size_t weight_bytes = 0;
+    const uint8_t* bias = nullptr;      // [lower] fp32
+};
+
+static int parse_record(const void* data, size_t bytes, LayerRecord* r) {
+    const uint8_t* p = (const uint8_t*)data;
+    const size_t header = 28;   // FixedHeaderBytes, :45
+    if (bytes < header) return fail(PCD_INVALID_VALUE, "layer record: %zu bytes is shorter than its header", bytes);
+    auto i32 = [&](size_t off) { int32_t v; std::memcpy(&v, p + off, 4); return v; };   // little-endian host
+    r->size = i32(0);
+    r->lower = i32(4);
+    std::memcpy(&r->precision, p + 8, 4);
+    r->flags = p[25];
+    if (r->size < 1 || r->lower < 0) return fail(PCD_INVALID_VALUE, "layer record: sizes (%d,%d)", r->size, r->lower);
+    if (r->flags & 3)
+        return fail(PCD_NOT_SUPPORTED, "layer record has a diagonal precision or a prior mean, which the "
+                                       "generative snapshot does not carry");
+    const int fmt = r->flags & (4 | 8 | 16);
+    if (fmt != 0 && fmt != 4 && fmt != 8 && fmt != 16)
+        return fail(PCD_INVALID_VALUE, "layer record: more than one weight format flag (0x%x)", r->flags);
+    r->kind = fmt == 4 ? REC_F16 : fmt == 8 ? REC_BF16 : fmt == 16 ? REC_I8 : REC_F32;
+    const size_t lo = (size_t)r->lower, sz = (size_t)r->size;
+    size_t n = header + sz * 8;   // Mu + PredictionError
+    if (lo > 0) {
+        r->weights = p + n;
+        r->weight_bytes = r->kind == REC_F32 ? lo * sz * 4 : r->kind == REC_I8 ? lo * 4 + lo + lo * sz : lo * sz * 2;
+        n += r->weight_bytes;
+        r->bias = p + n;
+        n += lo * 4 * 3;          // Bias, PreActivation, Prediction
+    }
+    if (bytes != n) return fail(PCD_INVALID_VALUE, "layer record: %zu bytes, the header implies %zu", bytes, n);
+    return PCD_SUCCESS;
+}
+
+// Weights (W_l and W_l^T in the operand type) and bias of layer `layer` from
+// a parsed record.
+static hipError_t upload_record_weights(pcd_model* m, int layer, const LayerRecord& r) {
+    const int lo = m->s[layer - 1], sz = m->s[layer];
+    void* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, r.weight_bytes);
+    if (e != hipSuccess) return e;
+    e = hipMemcpy(tmp, r.weights, r.weight_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(m->bias[layer], r.bias, (size_t)lo * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        const float* scales = r.kind == REC_I8 ? (const float*)tmp : nullptr;
+        const int8_t* zeros = r.kind == REC_I8 ? (const int8_t*)tmp + (size_t)lo * 4 : nullptr;
+        const void* codes = r.kind == REC_I8 ? (const void*)((const int8_t*)tmp + (size_t)lo * 5) : tmp;
+        const int Rlo = (int)round_up(lo, kRowPad), Rsz = (int)round_up(sz, kRowPad);
+        const int g1 = (int)std::min<size_t>(((size_t)Rlo * m->P[layer] + 255) / 256, 8192);
+        const int g2 = (int)std::min<size_t>(((size_t)Rsz * m->P[layer - 1] + 255) / 256, 8192);
+        // W_l as stored ([lo x sz] -> [Rlo x P_l]) and transposed ([sz x lo] -> [Rsz x P_{l-1}]).
+        switch (m->dtype) {
+        case PCD_F32:
+            hipLaunchKernelGGL(pack_record_kernel<float>, dim3(g1), dim3(256), 0, 0, codes, r.kind, scales, zeros, lo,
+                               sz, 0, m->W[layer], Rlo, m->P[layer]);
+            hipLaunchKernelGGL(pack_record_kernel<float>, dim3(g2), dim3(256), 0, 0, codes, r.kind, scales, zeros, sz,
+                               lo, 1, m->WT[layer], Rsz, m->P[layer - 1]);
+            break;
+        case PCD_BF16:
+            hipLaunchKernelGGL(pack_record_kernel<bf16_t>, dim3(g1), dim3(256), 0, 0, codes, r.kind, scales, zeros, lo,
+                               sz, 0, m->W[layer], Rlo, m->P[layer]);
+            hipLaunchKernelGGL(pack_record_kernel<bf16_t>, dim3(g2), dim3(256), 0, 0, codes, r.kind, scales, zeros, sz,
+                               lo, 1, m->WT[layer], Rsz, m->P[layer - 1]);
+            break;
+        default:
+            hipLaunchKernelGGL(pack_record_kernel<f16_t>, dim3(g1), dim3(256), 0, 0, codes, r.kind, scales, zeros, lo,
+                               sz, 0, m->W[layer], Rlo, m->P[layer]);
+            hipLaunchKernelGGL(pack_record_kernel<f16_t>, dim3(g2), dim3(256), 0, 0, codes, r.kind, scales, zeros, sz,
+                               lo, 1, m->WT[layer], Rsz, m->P[layer - 1]);
+            break;
+        }
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+    }
+    (void)hipFree(tmp);
+    return e;
+}
+
+int pcd_pc_model_load_record(pcd_model* m, int layer, const void* record, size_t bytes) {
+    if (int st = check_model(m)) return st;
+    if (!record) return fail(PCD_INVALID_VALUE, "pcd_pc_model_load_record: null record");
+    if (layer < 0 || layer >= m->L) return fail(PCD_INVALID_VALUE, "layer %d is not in 0..%d", layer, m->L - 1);
+    LayerRecord r;
+    if (int st = parse_record(record, bytes, &r)) return st;
+    const int lo = layer ? m->s[layer - 1] : 0, sz = m->s[layer];
+    if (r.size != sz || r.lower != lo)
+        return fail(PCD_INVALID_VALUE, "Layer size mismatch: stored (%d,%d) vs target (%d,%d).", r.size, r.lower, sz, lo);
+    if (!(r.precision > 0.f)) return fail(PCD_INVALID_VALUE, "layer record: precision %g is not positive", r.precision);
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(hipDeviceSynchronize());   // no settling may read the weights while they change
+    hipError_t e = hipSuccess;
+    if (layer > 0) e = upload_record_weights(m, layer, r);
+    if (e != hipSuccess) return from_hip(e, "pcd_pc_model_load_record");
+    m->prec[layer] = r.precision;
+    // cached graphs carry the precisions in their launch arguments
+    for (auto& w : m->ws) {
+        for (auto& p : w->plans) {
+            if (p->exec) (void)hipGraphExecDestroy(p->exec);
+            if (p->graph) (void)hipGraphDestroy(p->graph);
+            if (p->energy_out) (void)hipFree(p->energy_out);
+        }
+        w->plans.clear();
+    }
+    return PCD_SUCCESS;
+}
+
 
 }  // extern "C"
