@@ -241,8 +241,11 @@ int pcd_pc_classify(pcd_model* model, const float* x0, int batch, int steps, flo
  * the call starts from (batch = 1 is exactly Learn).  Device pointers:
  *   x0 [batch x sizes[0]], labels [batch x sizes[levels-1]],
  *   out_energy nullable [batch], each sample's energy at the last step.
- * fp32 models only (PCD_NOT_SUPPORTED otherwise).  The model's weights change:
- * no other call on the model may run concurrently (any stream).
+ * A 16-bit model keeps fp32 master weights and updates those, then re-rounds
+ * its operands: Network.LearnMixed (Network.cs:158-181); its delta is the
+ * 16-bit value the settling's W^T GEMM consumed (the reference's per-sample
+ * path keeps it fp32).  The model's weights change: no other call on the model
+ * may run concurrently (any stream).
  * Asynchronous on `stream`. */
 int pcd_pc_learn(pcd_model* model, const float* x0, const float* labels, int batch, int steps, float eta_w,
                  float weight_decay, float* out_energy, void* stream);
@@ -250,7 +253,7 @@ int pcd_pc_learn(pcd_model* model, const float* x0, const float* labels, int bat
 /* Reads layer `layer`'s (1..levels-1) current weights back to host memory, as
  * Network.ExportGenerativeSnapshot copies them (Network.cs:1328-1356):
  *   W_out  nullable host [sizes[layer-1] x sizes[layer]] (16-bit models give
- *          their operand values widened to fp32)
+ *          their fp32 master weights)
  *   b_out  nullable host [sizes[layer-1]]
  * Waits for the device. */
 int pcd_pc_model_get_weights(pcd_model* model, int layer, float* W_out, float* b_out);

@@ -534,16 +534,20 @@ int pco_classify(const int* sizes, int levels, int act, float eta, float act_reg
  *   W_l += eta_w delta_l (x) mu_l ;  b_l += eta_w delta_l ;  W_l -= eta_w lambda W_l.
  * A batch of B samples applies the sum of the B per-sample updates, all taken
  * at the weights before the call (B = 1 is exactly Learn).
+ * With a 16-bit round_mode the settling runs on rounded operands and the fp32
+ * W_all are the master weights, Network.LearnMixed's scheme (Network.cs:158-181);
+ * delta is then taken as the settling's W^T GEMM consumed it, rounded to the
+ * operand type (the reference's per-sample path keeps it fp32).
  * W_all and b_all are updated in place; out_energy [batch] (nullable) is each
  * sample's energy at the last step (the ComputeEnergy the trainer reads).
  */
 int pco_learn(const int* sizes, int levels, int act, float eta, float act_reg, int ffg,
-              float* W_all, float* b_all, const float* prec,
+              float* W_all, float* b_all, const float* prec, int round_mode,
               const float* x0, const float* labels, int batch, int steps,
               float eta_w, float weight_decay, float* out_energy) {
     if (levels < 2 || batch < 1 || steps < 1) return -1;
     model_t md;
-    setup_model(&md, sizes, levels, act, eta, act_reg, ffg, W_all, b_all, prec, ROUND_NONE);
+    setup_model(&md, sizes, levels, act, eta, act_reg, ffg, W_all, b_all, prec, round_mode);
     md.clamp_top = 1;
     const int L = levels;
     float** m = calloc((size_t)L, sizeof(float*));
@@ -560,6 +564,7 @@ int pco_learn(const int* sizes, int levels, int act, float eta, float act_reg, i
         float* W = (float*)w_of(&md, l);
         float* bb = (float*)b_of(&md, l);
         const int lo = sizes[l - 1], sz = sizes[l];
+        if (round_mode != ROUND_NONE) pco_round(round_mode, d[l], d[l], (long)batch * lo);
         float* dW = calloc((size_t)lo * sz, sizeof(float));
         float* db = calloc((size_t)lo, sizeof(float));
         for (int r = 0; r < batch; r++) {                   /* OuterProduct(delta, mu), summed */

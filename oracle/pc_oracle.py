@@ -71,7 +71,8 @@ def lib():
         L.pco_classify.restype = ctypes.c_int
         L.pco_learn.argtypes = [
             _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
-            _f32p, _f32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, _vp]
+            _f32p, _f32p, _f32p, ctypes.c_int, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+            ctypes.c_float, _vp]
         L.pco_learn.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -255,10 +256,10 @@ def classify(sizes, act, eta, weights, biases, precisions, x0, steps, act_reg=0.
 
 
 def learn(sizes, act, eta, weights, biases, precisions, x0, labels, steps, eta_w, weight_decay=0.0,
-          act_reg=0.0, ffg=False):
+          act_reg=0.0, ffg=False, round_mode="none"):
     """Network.Learn on a batch (B = 1 is the reference call; B > 1 sums the
-    per-sample updates at the pre-call weights).  Returns (new weights, new
-    biases, energy [B])."""
+    per-sample updates at the pre-call weights); with a 16-bit round_mode,
+    LearnMixed on fp32 masters.  Returns (new weights, new biases, energy [B])."""
     sizes = np.ascontiguousarray(sizes, dtype=np.int32)
     x0 = np.ascontiguousarray(x0, dtype=np.float32)
     B = x0.shape[0]
@@ -267,7 +268,8 @@ def learn(sizes, act, eta, weights, biases, precisions, x0, labels, steps, eta_w
     b = _flat(biases, np.float32).copy()
     energy = np.empty(B, dtype=np.float32)
     rc = lib().pco_learn(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg), W, b,
-                         np.ascontiguousarray(precisions, dtype=np.float32), x0.ravel(), labels.ravel(),
+                         np.ascontiguousarray(precisions, dtype=np.float32), ROUND[round_mode], x0.ravel(),
+                         labels.ravel(),
                          B, int(steps), float(eta_w), float(weight_decay), _ptr(energy))
     if rc != 0:
         raise ValueError("oracle rejected arguments")

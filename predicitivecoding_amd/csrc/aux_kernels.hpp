@@ -167,11 +167,13 @@ __global__ void class_argmin_kernel(const float* __restrict__ e, int batch, int 
 
 // Bias step of the learning rule (Layer.cs:327): b[i] += eta_w * sum over the
 // batch rows of D[r][i], rows summed in order.
-__global__ void bias_update_kernel(const float* __restrict__ d, int ld, int rows, int cols, float* __restrict__ bias,
+// D is in the operand type (16-bit models keep it 16-bit).
+template <typename OP>
+__global__ void bias_update_kernel(const void* __restrict__ d, int ld, int rows, int cols, float* __restrict__ bias,
                                    float eta_w) {
     for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x) {
         float s = 0.f;
-        for (int r = 0; r < rows; ++r) s += d[(size_t)r * ld + c];
+        for (int r = 0; r < rows; ++r) s += OpTraits<OP>::load(d, (size_t)r * ld + c);
         bias[c] += eta_w * s;
     }
 }

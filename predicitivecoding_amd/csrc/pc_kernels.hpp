@@ -214,14 +214,21 @@ template <typename OP> struct OpTraits;
 template <> struct OpTraits<float> {
     static constexpr int bytes = 4;
     __device__ static void store(void* base, size_t idx, float v) { gst((float*)base + idx, v); }
+    __device__ static float load(const void* base, size_t idx) { return ((const float*)base)[idx]; }
 };
 template <> struct OpTraits<bf16_t> {
     static constexpr int bytes = 2;
     __device__ static void store(void* base, size_t idx, float v) { gst((uint16_t*)base + idx, to_bf16(v)); }
+    __device__ static float load(const void* base, size_t idx) {
+        return __uint_as_float((uint32_t)((const uint16_t*)base)[idx] << 16);
+    }
 };
 template <> struct OpTraits<f16_t> {
     static constexpr int bytes = 2;
     __device__ static void store(void* base, size_t idx, float v) { gst((uint16_t*)base + idx, to_f16(v)); }
+    __device__ static float load(const void* base, size_t idx) {
+        return (float)__builtin_bit_cast(_Float16, ((const uint16_t*)base)[idx]);
+    }
 };
 
 // One 32-byte K chunk of a 32x32 block with 16-bit operands: a and b hold

@@ -255,6 +255,7 @@ struct pcd_model {
     float eta = 0.f, act_reg = 0.f;
     std::vector<float> prec;
     std::vector<void*> W, WT;           // [L] operand type; W[l] is [R(s_{l-1}) x P_l], WT[l] [R(s_l) x P_{l-1}]
+    std::vector<float*> W32;            // [L] fp32 master weights of 16-bit models, laid out as W[l]
     std::vector<float*> bias;           // [L] fp32 [P_{l-1}]
     std::mutex mu;
     std::vector<std::unique_ptr<Workspace>> ws;
@@ -1058,6 +1059,7 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
     m->prec.assign(precisions, precisions + levels);
     m->W.assign(levels, nullptr);
     m->WT.assign(levels, nullptr);
+    m->W32.assign(levels, nullptr);
     m->bias.assign(levels, nullptr);
     const int ob = op_bytes(dtype);
     std::vector<void*> owned;
@@ -1076,6 +1078,15 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
         m->W[l] = w;
         m->WT[l] = wt;
         m->bias[l] = (float*)bb;
+        if (dtype != PCD_F32) {
+            // fp32 masters, which the learning step updates (Network.LearnMixed's scheme)
+            void* w32 = nullptr;
+            if ((st = dev_alloc_zero(owned, &w32, (size_t)Rlo * m->P[l] * 4))) {
+                cleanup();
+                return st;
+            }
+            m->W32[l] = (float*)w32;
+        }
         if (!W) continue;   // zero weights, to be filled by pcd_pc_model_load_record
         if ((st = dev_alloc_zero(owned, &tmp, (size_t)lo * sz * 4))) {
             cleanup();
@@ -1101,6 +1112,9 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
             hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
             break;
         }
+        if (m->W32[l])
+            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, m->W32[l], Rlo,
+                               m->P[l], m->P[l]);
         e = hipGetLastError();
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) { cleanup(); return from_hip(e, "weight packing"); }
@@ -1119,6 +1133,7 @@ int pcd_pc_model_destroy(pcd_model* m) {
         (void)hipFree(m->W[l]);
         (void)hipFree(m->WT[l]);
         (void)hipFree(m->bias[l]);
+        if (m->W32[l]) (void)hipFree(m->W32[l]);
     }
     delete m;
     return PCD_SUCCESS;
@@ -1320,6 +1335,36 @@ static int stage_top(pcd_model* m, Workspace* w, const float* src, int rows, hip
     return from_hip(hipGetLastError(), "top_rows_kernel launch");
 }
 
+// After the fp32 weights of layer l changed (the fp32 W itself, or a 16-bit
+// model's masters W32): W^T, and for 16-bit models W, re-derived in the
+// operand type (rounded to nearest even).
+static int refresh_operands(pcd_model* m, int l, hipStream_t s) {
+    const int lo = m->s[l - 1], sz = m->s[l];
+    const int Rlo = (int)round_up(lo, kRowPad), Rsz = (int)round_up(sz, kRowPad);
+    const void* src = m->dtype == PCD_F32 ? (const void*)m->W[l] : (const void*)m->W32[l];
+    const int g1 = (int)std::min<size_t>(((size_t)Rlo * m->P[l] + 255) / 256, 8192);
+    const int g2 = (int)std::min<size_t>(((size_t)Rsz * m->P[l - 1] + 255) / 256, 8192);
+    switch (m->dtype) {
+    case PCD_F32:
+        hipLaunchKernelGGL(pack_kernel<float>, dim3(g2), dim3(256), 0, s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
+                           m->P[l - 1], m->P[l - 1]);
+        break;
+    case PCD_BF16:
+        hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(g1), dim3(256), 0, s, src, 1, Rlo, m->P[l], 0, m->W[l], Rlo,
+                           m->P[l], m->P[l]);
+        hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(g2), dim3(256), 0, s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
+                           m->P[l - 1], m->P[l - 1]);
+        break;
+    default:
+        hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(g1), dim3(256), 0, s, src, 1, Rlo, m->P[l], 0, m->W[l], Rlo,
+                           m->P[l], m->P[l]);
+        hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(g2), dim3(256), 0, s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
+                           m->P[l - 1], m->P[l - 1]);
+        break;
+    }
+    return from_hip(hipGetLastError(), "operand refresh");
+}
+
 int pcd_pc_relax_clamped(pcd_model* m, const float* x0, const float* top, int batch, int steps, float* out_states,
                          float* out_energy, void* stream_) {
     if (int st = check_model(m)) return st;
@@ -1393,8 +1438,6 @@ int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, 
     if (batch < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
     if (steps < 1) return fail(PCD_INVALID_VALUE, "inferenceSteps must be >= 1, got %d", steps);
     if (!x0 || !labels) return fail(PCD_INVALID_VALUE, "pcd_pc_learn: null pointer");
-    if (m->dtype != PCD_F32)
-        return fail(PCD_NOT_SUPPORTED, "pcd_pc_learn: the learning step updates fp32 weights (model is 16-bit)");
     hipStream_t s = (hipStream_t)stream_;
     std::lock_guard<std::mutex> g(m->mu);
     HIP_TRY(hipSetDevice(m->device));
@@ -1434,15 +1477,32 @@ int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, 
         tmp.push_back(mt);
         const int g1 = (int)std::min<size_t>(((size_t)Rlo * kp + 255) / 256, 8192);
         const int g2 = (int)std::min<size_t>(((size_t)Rsz * kp + 255) / 256, 8192);
-        hipLaunchKernelGGL(pack_kernel<float>, dim3(g1), dim3(256), 0, s, (const void*)w->D[l], 1, m->P[l - 1], batch,
-                           1, dt, Rlo, kp, kp);
+        const int gb = std::min((lo + 255) / 256, 1024);
+        // D_l^T (D is in the operand type: a 16-bit model's update uses the
+        // rounded Delta its settling's W^T GEMM consumed), M_l^T, and the bias
+        switch (m->dtype) {
+        case PCD_F32:
+            hipLaunchKernelGGL(pack_kernel<float>, dim3(g1), dim3(256), 0, s, (const void*)w->D[l], 1, m->P[l - 1],
+                               batch, 1, dt, Rlo, kp, kp);
+            hipLaunchKernelGGL(bias_update_kernel<float>, dim3(gb), dim3(256), 0, s, (const void*)w->D[l],
+                               m->P[l - 1], batch, lo, m->bias[l], eta_w);
+            break;
+        case PCD_BF16:
+            hipLaunchKernelGGL(pack_record_kernel<float>, dim3(g1), dim3(256), 0, s, (const void*)w->D[l],
+                               (int)REC_BF16, nullptr, nullptr, m->P[l - 1], batch, 1, dt, Rlo, kp);
+            hipLaunchKernelGGL(bias_update_kernel<bf16_t>, dim3(gb), dim3(256), 0, s, (const void*)w->D[l],
+                               m->P[l - 1], batch, lo, m->bias[l], eta_w);
+            break;
+        default:
+            hipLaunchKernelGGL(pack_record_kernel<float>, dim3(g1), dim3(256), 0, s, (const void*)w->D[l],
+                               (int)REC_F16, nullptr, nullptr, m->P[l - 1], batch, 1, dt, Rlo, kp);
+            hipLaunchKernelGGL(bias_update_kernel<f16_t>, dim3(gb), dim3(256), 0, s, (const void*)w->D[l],
+                               m->P[l - 1], batch, lo, m->bias[l], eta_w);
+            break;
+        }
         hipLaunchKernelGGL(pack_kernel<float>, dim3(g2), dim3(256), 0, s, (const void*)w->M[l], 1, m->P[l], batch, 1,
                            mt, Rsz, kp, kp);
-        if ((st = from_hip(hipGetLastError(), "pack_kernel launch"))) break;
-        const int gb = std::min((lo + 255) / 256, 1024);
-        hipLaunchKernelGGL(bias_update_kernel, dim3(gb), dim3(256), 0, s, (const float*)w->D[l], m->P[l - 1], batch,
-                           lo, m->bias[l], eta_w);
-        if ((st = from_hip(hipGetLastError(), "bias_update_kernel launch"))) break;
+        if ((st = from_hip(hipGetLastError(), "learning-step packing"))) break;
         if (sets.empty() || sets.back().n == kMaxProblems) {
             sets.emplace_back();
             std::memset(&sets.back(), 0, sizeof(ProblemSet));
@@ -1459,7 +1519,7 @@ int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, 
         p.tiles_n = (sz + tile.n - 1) / tile.n;
         p.tiles = p.tiles_m * p.tiles_n;
         p.ldo = m->P[l];
-        p.m = (float*)m->W[l];
+        p.m = m->dtype == PCD_F32 ? (float*)m->W[l] : m->W32[l];   // fp32 weights or masters
     }
     if (!st) {
         const float keep = 1.f - eta_w * weight_decay;
@@ -1471,14 +1531,7 @@ int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, 
         for (auto& ps : sets)
             if ((st = launch_phase(PCD_F32, tile, EPI_PLAIN, ps, a, s))) break;
     }
-    for (int l = 1; l < L && !st; ++l) {
-        const int lo = m->s[l - 1], sz = m->s[l];
-        const int Rsz = (int)round_up(sz, kRowPad);
-        const int g = (int)std::min<size_t>(((size_t)Rsz * m->P[l - 1] + 255) / 256, 8192);
-        hipLaunchKernelGGL(pack_kernel<float>, dim3(g), dim3(256), 0, s, (const void*)m->W[l], 1, m->P[l], lo, 1,
-                           m->WT[l], Rsz, m->P[l - 1], m->P[l - 1]);
-        st = from_hip(hipGetLastError(), "pack_kernel launch (W^T)");
-    }
+    for (int l = 1; l < L && !st; ++l) st = refresh_operands(m, l, s);
     for (void* t : tmp) {
         int st2 = pool_free(t, s);
         if (!st) st = st2;
@@ -1498,24 +1551,9 @@ int pcd_pc_model_get_weights(pcd_model* m, int layer, float* W_out, float* b_out
     HIP_TRY(hipDeviceSynchronize());
     const int lo = m->s[layer - 1], sz = m->s[layer];
     if (W_out) {
-        if (m->dtype == PCD_F32) {
-            HIP_TRY(hipMemcpy2D(W_out, (size_t)sz * 4, m->W[layer], (size_t)m->P[layer] * 4, (size_t)sz * 4, lo,
-                                hipMemcpyDeviceToHost));
-        } else {
-            std::vector<uint16_t> bits((size_t)lo * sz);
-            HIP_TRY(hipMemcpy2D(bits.data(), (size_t)sz * 2, m->W[layer], (size_t)m->P[layer] * 2, (size_t)sz * 2, lo,
-                                hipMemcpyDeviceToHost));
-            for (size_t i = 0; i < bits.size(); ++i) {
-                if (m->dtype == PCD_BF16) {
-                    const uint32_t u = (uint32_t)bits[i] << 16;
-                    std::memcpy(&W_out[i], &u, 4);
-                } else {
-                    _Float16 h;
-                    std::memcpy(&h, &bits[i], 2);
-                    W_out[i] = (float)h;
-                }
-            }
-        }
+        const void* src = m->dtype == PCD_F32 ? (const void*)m->W[layer] : (const void*)m->W32[layer];
+        HIP_TRY(hipMemcpy2D(W_out, (size_t)sz * 4, src, (size_t)m->P[layer] * 4, (size_t)sz * 4, lo,
+                            hipMemcpyDeviceToHost));
     }
     if (b_out) HIP_TRY(hipMemcpy(b_out, m->bias[layer], (size_t)lo * 4, hipMemcpyDeviceToHost));
     return PCD_SUCCESS;
@@ -1601,6 +1639,9 @@ static hipError_t upload_record_weights(pcd_model* m, int layer, const LayerReco
                                lo, 1, m->WT[layer], Rsz, m->P[layer - 1]);
             break;
         }
+        if (m->W32[layer])
+            hipLaunchKernelGGL(pack_record_kernel<float>, dim3(g1), dim3(256), 0, 0, codes, r.kind, scales, zeros, lo,
+                               sz, 0, m->W32[layer], Rlo, m->P[layer]);
         e = hipGetLastError();
         if (e == hipSuccess) e = hipDeviceSynchronize();
     }

@@ -187,13 +187,44 @@ def test_train_two_patterns_then_predict(oracle):
     assert max_rel(ce, rce) < 1e-4 and list(rcls) == [0, 1]
 
 
-def test_learn_rejects_16bit_model():
-    from predicitivecoding_amd.errors import DeviceException, DeviceStatus
-    snap, _, _, _, x = build_case([8, 6, 3], "tanh", 0.1, batch=2, seed=16)
-    m = _model(snap, "bf16")
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_learn_step_16bit_masters(oracle, dtype):
+    # LearnMixed's scheme: 16-bit settling, fp32 master update, operands re-rounded
+    sizes = [37, 70, 19, 6]
+    snap, W, b, P, x = build_case(sizes, "gelu", 0.1, batch=9, bias_scale=0.1, seed=17)
+    y = _one_hot(np.arange(9) % 6, 6)
+    m = _model(snap, dtype)
     try:
-        with pytest.raises(DeviceException) as ei:
-            m.learn(x, _one_hot([0, 1], 3), 3, 0.01)
-        assert ei.value.code == DeviceStatus.NotSupported
+        en = m.learn(x, y, 8, 0.05)
+        gw, gb = m.get_weights()
+        _, en2 = m.relax_clamped(x, y, 5)
     finally:
         m.close()
+    rw, rb, ren = oracle.learn(sizes, "gelu", 0.1, W, b, P, x, y, 8, 0.05, round_mode=dtype)
+    _, ren2 = oracle.clamped_relax(sizes, "gelu", 0.1, rw, rb, P, x, y, 5, round_mode=dtype)
+    errs = dict(weights=max(max_rel(a, r) for a, r in zip(gw, rw)), biases=max(max_rel(a, r) for a, r in zip(gb, rb)),
+                energy=max_rel(en, ren), energy_after=max_rel(en2, ren2))
+    _report(f"learn {dtype}", **errs)
+    assert all(v < 2e-3 for v in errs.values()), errs
+
+
+def test_learn_mixed_predicts_like_float(oracle):
+    # NetworkTests' mixed-precision contract: the bf16 model trained with
+    # LearnMixed's scheme classifies the two patterns like the fp32 network
+    sizes = [4, 8, 2]
+    W, b, P = make_net(sizes, seed=42)
+    from predicitivecoding_amd import GenerativeSnapshot
+    snap = GenerativeSnapshot(sizes, ACT["tanh"], 0.1, 0.0, False, W, b, list(P))
+    a = np.array([[1, 0, 0, 0]], np.float32)
+    bb = np.array([[0, 0, 0, 1]], np.float32)
+    m = _model(snap, "bf16")
+    try:
+        for _ in range(40):
+            m.learn(a, _one_hot([0], 2), 30, 0.01)
+            m.learn(bb, _one_hot([1], 2), 30, 0.01)
+        gw, _ = m.get_weights()
+        _, cls, _ = m.classify(np.concatenate([a, bb]), 15)
+    finally:
+        m.close()
+    assert list(cls) == [0, 1]
+    assert all(np.all(np.isfinite(w)) for w in gw)

@@ -176,3 +176,19 @@ def test_trained_class_energies_mixed_track_float(oracle):
     half, bch, _ = oracle.classify(sizes, "tanh", 0.2, W, b, P, xs, 20, round_mode="f16")
     assert np.all(np.abs(full - half) <= 5e-2 * (1 + np.abs(full)))
     assert list(bc) == list(bch) == [0, 1]
+
+
+@pytest.mark.parametrize("mode", ["bf16", "f16"])
+def test_mixed_learn_tracks_float_learn(oracle, mode):
+    # LearnMixed differs from Learn only by the 16-bit settling (and its rounded
+    # delta): the updated masters stay within half precision's tolerance
+    sizes = [6, 9, 4]
+    W, b, P = make_net(sizes, seed=71, bias_scale=0.1)
+    x = make_inputs(5, 6, seed=72)
+    y = one_hot([0, 3, 1, 2, 3], 4)
+    fw, fb, fe = oracle.learn(sizes, "tanh", 0.1, W, b, P, x, y, 10, 0.05)
+    mw, mb, me = oracle.learn(sizes, "tanh", 0.1, W, b, P, x, y, 10, 0.05, round_mode=mode)
+    for l in range(2):
+        assert close(mw[l], fw[l], 2e-2) and close(mb[l], fb[l], 2e-2)
+        assert not np.array_equal(mw[l], fw[l])      # the rounding is really applied
+    assert close(me, fe, 5e-2)
