@@ -352,18 +352,27 @@ int split_part_tiles(const pcd_model* m) { return std::max(m->cus, 1); }
 #endif
 constexpr int kSplitMinStages = PCD_SPLIT_MIN_STAGES;
 
-int split_factor(const pcd_model* m, long tiles, Tile tile) {
-    if (!m->split_k || tile.m * tile.n > 128 * 128 || tiles < 1 || tiles * 2 > m->cus) return 1;
-    return (int)std::min<long>(kMaxSplit, m->cus / tiles);
+int split_factor(int cus, int split_k, long tiles, Tile tile) {
+    if (!split_k || tile.m * tile.n > 128 * 128 || tiles < 1 || tiles * 2 > cus) return 1;
+    return (int)std::min<long>(kMaxSplit, cus / tiles);
 }
 
-// K elements of one LDS stage of `tile` for the model's operand type.
-int stage_k(const pcd_model* m, Tile tile) {
+// K elements of one LDS stage of `tile` for an operand type.
+int stage_k(int dtype, Tile tile) {
     int rb = 64;
     if (tile.m == 128 && tile.n == 128) rb = TileCfg<128, 128>::RB;
     else if (tile.m == 256 && tile.n == 256) rb = TileCfg<256, 256>::RB;
-    return rb / op_bytes(m->dtype);
+    return rb / op_bytes(dtype);
 }
+
+// The split-K plan of a phase or a GEMM: every problem's split factor and its
+// share of the partial-tile scratch (`part`, room for `budget` tiles of up to
+// 128 x 128) and of the counters (`count`, as many).
+struct SplitScratch {
+    float* part = nullptr;
+    int* count = nullptr;
+    long budget = 0;
+};
 
 // Gives every problem of a phase its split factor and its share of the scratch.
 // Besides the few-tiles split of the whole phase, a problem whose eighth (one
@@ -371,12 +380,12 @@ int stage_k(const pcd_model* m, Tile tile) {
 // per CU: its tiles would otherwise give a part of the CUs one more whole tile
 // than the rest (c2's update phase: 8 tiles of the 256-wide layer per XCD of 32
 // CUs next to 3 x 32 full tiles).  Splitting stops where the scratch is spent.
-void assign_split(const pcd_model* m, const Workspace* w, Tile tile, std::vector<ProblemSet>& sets) {
+void assign_split(int cus, int split_k, int dtype, Tile tile, const SplitScratch& sc, std::vector<ProblemSet>& sets) {
     long tiles = 0;
     for (auto& ps : sets)
         for (int i = 0; i < ps.n; ++i) tiles += (long)ps.p[i].tiles_m * ps.p[i].tiles_n;
-    const int f = split_factor(m, tiles, tile);
-    const int per_xcd = std::max(1, m->cus / kXcds);
+    const int f = split_factor(cus, split_k, tiles, tile);
+    const int per_xcd = std::max(1, cus / kXcds);
     const bool small_tile = tile.m * tile.n <= 128 * 128;
     long units = 0, counters = 0;
     for (auto& ps : sets)
@@ -384,19 +393,20 @@ void assign_split(const pcd_model* m, const Workspace* w, Tile tile, std::vector
             Problem& p = ps.p[i];
             const int t = p.tiles_m * p.tiles_n;
             const int share = (t + kXcds - 1) / kXcds;
-            const int fb = (m->split_k && small_tile && share < per_xcd) ? per_xcd / share : 1;
-            int ks = std::max(1, std::min({std::max(f, fb), kMaxSplit, p.K / stage_k(m, tile) / kSplitMinStages}));
-            if (ks > 1 && units + (long)t * ks > split_part_tiles(m)) ks = 1;
+            const int fb = (split_k && small_tile && share < per_xcd) ? per_xcd / share : 1;
+            int ks = std::max(1, std::min({std::max(f, fb), kMaxSplit, p.K / stage_k(dtype, tile) / kSplitMinStages}));
+            if (ks > 1 && units + (long)t * ks > sc.budget) ks = 1;
             p.ksplit = ks;
             p.tiles = t * ks;
             if (ks > 1) {
-                p.part = w->split_part + units * (long)tile.m * tile.n;
-                p.count = w->split_count + counters;
+                p.part = sc.part + units * (long)tile.m * tile.n;
+                p.count = sc.count + counters;
                 units += (long)t * ks;
                 counters += t;
             }
         }
 }
+
 
 int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out) {
     Workspace* w = nullptr;
@@ -501,8 +511,12 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         p.mop = m->dtype == PCD_F32 ? nullptr : w->S[l];
         p.eself = l <= L - 2 ? w->E[l] : nullptr;
     }
-    assign_split(m, w, tile, err);
-    assign_split(m, w, tile, upd);
+    SplitScratch sc;
+    sc.part = w->split_part;
+    sc.count = w->split_count;
+    sc.budget = split_part_tiles(m);
+    assign_split(m->cus, m->split_k, m->dtype, tile, sc, err);
+    assign_split(m->cus, m->split_k, m->dtype, tile, sc, upd);
     *nslots = slot;
 }
 
@@ -945,18 +959,39 @@ int pcd_event_elapsed_ms(float* ms, void* start, void* end) {
 
 // -------------------------------------------------------------------- GEMM
 
+// Output tile of a provider GEMM: 256 x 256 (16-bit operands) while it still
+// gives every CU a tile, then 128 x 128 while that does, else 64 x 64 (whose
+// few tiles split-K then spreads over the CUs).
+static Tile choose_gemm_tile(int dtype, int m, int n, int cus) {
+    auto tiles = [&](int t) { return (long)((m + t - 1) / t) * ((n + t - 1) / t); };
+    if (dtype != PCD_F32 && tiles(256) >= cus) return Tile{256, 256};
+    if (tiles(128) >= cus) return Tile{128, 128};
+    return Tile{64, 64};
+}
+
 static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int m, int k, int n, int trans_a,
                        int trans_b, float beta, void* stream_) {
     if (!dA || !dB || !dC) return fail(PCD_INVALID_VALUE, "pcd_gemm: null pointer");
     if (m < 1 || k < 1 || n < 1) return fail(PCD_INVALID_VALUE, "pcd_gemm: bad shape %d x %d x %d", m, k, n);
     hipStream_t s = (hipStream_t)stream_;
-    const Tile tile = (m <= 64 || n <= 64) ? Tile{64, 64} : Tile{128, 128};
+    int dev = 0, cus = 256;
+    HIP_TRY(hipGetDevice(&dev));
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const Tile tile = choose_gemm_tile(dtype, m, n, cus);
     const int mp = (int)round_up(m, tile.m), np = (int)round_up(n, tile.n), kp = (int)round_up(k, kFeatPad);
     const int ob = op_bytes(dtype);
+    // An operand already K-contiguous, with whole tiles of rows, K a whole
+    // number of stages and 16-byte aligned rows, is read where it lies; any
+    // other is packed into zero-padded scratch.
+    auto aligned = [&](const void* p) { return ((uintptr_t)p % 16) == 0; };
+    const bool direct_a = !trans_a && m == mp && k == kp && aligned(dA);
+    const bool direct_b = trans_b && n == np && k == kp && aligned(dB);
     void *pa = nullptr, *pb = nullptr;
-    int st;
-    if ((st = pool_alloc(&pa, (size_t)mp * kp * ob, s))) return st;
-    if ((st = pool_alloc(&pb, (size_t)np * kp * ob, s))) { pool_free(pa, s); return st; }
+    int st = PCD_SUCCESS;
+    auto release = [&]() {
+        if (pa && !direct_a) pool_free(pa, s);
+        if (pb && !direct_b) pool_free(pb, s);
+    };
     const int src_f32 = dtype == PCD_F32;
     auto pack = [&](const void* src, int rows, int cols, int trans, void* dst, int prow, int pcol) -> int {
         int grid = (int)std::min<size_t>(((size_t)prow * pcol + 255) / 256, 8192);
@@ -970,15 +1005,16 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     // op(A) [m x k]: physical [m x k], or [k x m] when transposed.
     // The kernel's B operand is op(B)^T [n x k]: physical B is [k x n] (read
     // transposed) or, with trans_b, already [n x k].
-    if ((st = pack(dA, m, k, trans_a, pa, mp, kp)) || (st = pack(dB, n, k, trans_b ? 0 : 1, pb, np, kp))) {
-        pool_free(pa, s);
-        pool_free(pb, s);
-        return st;
+    if (direct_a) pa = (void*)dA;
+    else if (!(st = pool_alloc(&pa, (size_t)mp * kp * ob, s))) st = pack(dA, m, k, trans_a, pa, mp, kp);
+    if (!st) {
+        if (direct_b) pb = (void*)dB;
+        else if (!(st = pool_alloc(&pb, (size_t)np * kp * ob, s))) st = pack(dB, n, k, trans_b ? 0 : 1, pb, np, kp);
     }
-    ProblemSet ps;
-    std::memset(&ps, 0, sizeof ps);
-    ps.n = 1;
-    Problem& p = ps.p[0];
+    std::vector<ProblemSet> sets(1);
+    std::memset(&sets[0], 0, sizeof(ProblemSet));
+    sets[0].n = 1;
+    Problem& p = sets[0].p[0];
     p.A = pa;
     p.lda = kp;
     p.B = pb;
@@ -991,17 +1027,31 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     p.tiles = p.tiles_m * p.tiles_n;
     p.ldo = n;
     p.m = dC;
+    // Split-K scratch from the pool; the counters start at zero (a fill
+    // kernel, so a captured call stays free of memset nodes).
+    SplitScratch sc;
+    void* part = nullptr;
+    if (!st && tile.m * tile.n <= 128 * 128 && p.tiles * 2 <= cus) {
+        sc.budget = cus;
+        const size_t part_bytes = (size_t)sc.budget * 128 * 128 * 4, cnt_bytes = round_up((size_t)sc.budget * 4, 16);
+        if (!(st = pool_alloc(&part, part_bytes + cnt_bytes, s))) {
+            sc.part = (float*)part;
+            sc.count = (int*)((char*)part + part_bytes);
+            st = launch_zero(sc.count, cnt_bytes, s);
+        }
+    }
+    if (!st) assign_split(cus, 1, dtype, tile, sc, sets);
     PhaseArgs a;
     std::memset(&a, 0, sizeof a);
     a.alpha = 1.f;
     a.beta = beta;
-    st = launch_phase(dtype, tile, EPI_PLAIN, ps, a, s);
-    int st2 = pool_free(pa, s);
-    int st3 = pool_free(pb, s);
-    if (st) return st;
-    if (st2) return st2;
-    if (st3) return fail(PCD_GEMM_ERROR, "pcd_gemm: scratch release failed");
-    return PCD_SUCCESS;
+    if (!st) st = launch_phase(dtype, tile, EPI_PLAIN, sets[0], a, s);
+    release();
+    if (part) {
+        int st2 = pool_free(part, s);
+        if (!st) st = st2;
+    }
+    return st;
 }
 
 int pcd_gemm_f32(const float* dA, const float* dB, float* dC, int m, int k, int n, int trans_a, int trans_b,

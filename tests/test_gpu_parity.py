@@ -281,3 +281,46 @@ def test_split_k_repeated_graph_replays():
             assert np.array_equal(first[0], again[0]) and np.array_equal(first[2], again[2])
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("dtype,m,k,n,ta,tb", [
+    ("f32", 64, 4096, 64, 0, 0),        # one output tile, long K: split over 8 workgroups
+    ("f32", 128, 2048, 192, 1, 1),      # transposed operands, split-K
+    ("bf16", 1024, 1024, 1024, 0, 1),   # both operands read where they lie (no packing)
+    ("bf16", 4096, 4096, 4096, 0, 0),   # 256 x 256 tiles
+    ("f16", 300, 777, 1000, 1, 0),      # ragged shape, packed
+])
+def test_gemm_provider_shapes(dtype, m, k, n, ta, tb):
+    # CudaGemmProvider.MatMulDeviceEx semantics (C = op(A) op(B) + beta C) on the
+    # tile, split-K and direct-operand paths, against float64 of the same
+    # operand values
+    import ctypes
+    from predicitivecoding_amd import DeviceTensor
+    from predicitivecoding_amd._native import call
+    rng = np.random.default_rng(7)
+    A = rng.standard_normal((k, m) if ta else (m, k)).astype(np.float32)
+    B = rng.standard_normal((n, k) if tb else (k, n)).astype(np.float32)
+    if dtype == "bf16":
+        from oracle import pc_oracle
+        Ab, Bb = pc_oracle.bf16_bits(A), pc_oracle.bf16_bits(B)
+        A = (Ab.astype(np.uint32) << 16).view(np.float32)
+        B = (Bb.astype(np.uint32) << 16).view(np.float32)
+        dA, dB = DeviceTensor.from_host(Ab), DeviceTensor.from_host(Bb)
+    elif dtype == "f16":
+        Ah, Bh = A.astype(np.float16), B.astype(np.float16)
+        A, B = Ah.astype(np.float32), Bh.astype(np.float32)
+        dA, dB = DeviceTensor.from_host(Ah.view(np.uint16)), DeviceTensor.from_host(Bh.view(np.uint16))
+    else:
+        dA, dB = DeviceTensor.from_host(A), DeviceTensor.from_host(B)
+    C0 = rng.standard_normal((m, n)).astype(np.float32)
+    dC = DeviceTensor.from_host(C0)
+    try:
+        call(f"pcd_gemm_{dtype}", dA.ptr, dB.ptr, dC.ptr, m, k, n, ta, tb, 0.25, None)
+        got = dC.to_host()
+    finally:
+        for t in (dA, dB, dC):
+            t.free()
+    want = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64) + 0.25 * C0
+    err = np.max(np.abs(got - want)) / (1 + np.max(np.abs(want)))
+    print(f"gemm {dtype} {m}x{k}x{n} ta={ta} tb={tb} err={err:.2e}", flush=True)
+    assert err < 1e-5
