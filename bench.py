@@ -19,6 +19,7 @@ Workloads:
            to each one-hot label); value counts the 640 settled rows x T.
   c1learn  c1's network taking a learning step (Network.Learn) on a batch of
            64 labelled samples; value counts 64 rows x T.
+  gemm     the GEMM provider (pcd_gemm_bf16) on 8192^3, in TFLOP/s.
 
 The JSON line carries the roofline of the dominant kernel (average duration
 of its launches from HIP events on the library's stream) and a CPU baseline:
@@ -57,6 +58,8 @@ CONFIGS = {
                   init="xavier", mode="classify"),
     "c1learn": dict(sizes=[784, 256, 256, 10], act=1, dtype="f32", batch=64, T=20, eta=0.1, x="uniform01",
                     init="xavier", mode="learn", eta_w=0.01),
+    # the GEMM provider slot (IGemmProvider / CudaGemmProvider.MatMulDeviceExBf16) on c5's layer shape
+    "gemm": dict(dtype="bf16", m=8192, k=8192, n=8192),
 }
 ACT_NAME = {1: "tanh", 4: "gelu"}
 
@@ -416,6 +419,76 @@ def cpu_baseline_clamped(cfg, W, b, x_host, labels_host, budget_s=10.0):
                       f"x {per_sample_rows} settlings x {T} steps, {dt:.1f} s"}
 
 
+def bench_gemm(args, cfg):
+    """gemm: one pass = one pcd_gemm_bf16 call, C = A B^T with both operands
+    already K-contiguous in HBM (read in place)."""
+    import torch
+    from predicitivecoding_amd import DeviceTensor  # noqa: F401  (loads the library)
+    from predicitivecoding_amd._native import call
+    m, k, n = cfg["m"], cfg["k"], cfg["n"]
+    print(f"# bench gemm: {cfg['dtype']} {m} x {k} x {n}", file=sys.stderr, flush=True)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    A = torch.randn((m, k), generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+    B = torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+    C = torch.empty((m, n), device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+
+    def one_pass():
+        call("pcd_gemm_bf16", A.data_ptr(), B.data_ptr(), C.data_ptr(), m, k, n, 0, 1, 0.0, None)
+
+    for _ in range(args.warmup):
+        one_pass()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_pass()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    flop = 2.0 * m * n * k
+    value = flop * args.steps / elapsed / 1e12
+    ms = elapsed * 1e3 / args.steps
+    # the launch itself, timed with events on the stream it runs on (the default stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        one_pass()
+    e1.record()
+    torch.cuda.synchronize()
+    kms = e0.elapsed_time(e1) / args.steps
+    achieved = flop / (kms * 1e-3)
+    print(f"# timed {args.steps} GEMMs: {ms:.3f} ms each, {value:.1f} TFLOP/s; kernel {kms:.3f} ms", file=sys.stderr,
+          flush=True)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import pc_oracle
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+        pc_oracle.set_threads(threads)
+        bt = B.float().cpu().numpy().T.copy()
+        t0 = time.perf_counter()
+        pc_oracle.gemm(A[:16].float().cpu().numpy(), bt, "bf16")     # calibration
+        per_row = (time.perf_counter() - t0) / 16
+        rows = int(min(m, max(16, args.cpu_budget / 2 / max(per_row, 1e-9))))
+        a = A[:rows].float().cpu().numpy()
+        t0 = time.perf_counter()
+        pc_oracle.gemm(a, bt, "bf16")
+        dt = time.perf_counter() - t0
+        cpu = {"value": 2.0 * rows * n * k / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+               "sample": f"oracle mixed GEMM (Gemm.cs:44-60, i-k-j row-parallel), {rows} of {m} rows, {dt:.1f} s"}
+        print(f"# cpu baseline: {cpu['value'] * 1e3:.2f} GFLOP/s on {threads} threads", file=sys.stderr, flush=True)
+    rec = {
+        "metric": "provider GEMM throughput at 1 GPU and % of MFMA roofline", "value": value, "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": cfg["dtype"], "data": "synthetic (seeded random operands)",
+        "config": {"workload": f"gemm: pcd_gemm_bf16 {m} x {k} x {n}, B given transposed (K-contiguous)",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[cfg["dtype"]] / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK[cfg["dtype"]], "traffic": None,
+                     "kernel": "phase_kernel EPI_PLAIN", "kernel_ms": kms},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec))
+
+
 def cpu_baseline_ragged(cfg, W, b, x_host, offsets, steps, budget_s=10.0):
     """The oracle's per-request relaxation with the same exit rule, on the
     first requests that fit the time budget."""
@@ -487,6 +560,9 @@ def main():
         return
     if "mode" in cfg:
         bench_clamped(args, cfg)
+        return
+    if args.config == "gemm":
+        bench_gemm(args, cfg)
         return
     sizes, B, T = cfg["sizes"], cfg["batch"], cfg["T"]
     print(f"# bench {args.config}: sizes={sizes} B={B} T={T} dtype={cfg['dtype']}", file=sys.stderr, flush=True)
