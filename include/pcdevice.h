@@ -284,6 +284,13 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *                1: every XCD runs one contiguous eighth of the phase's tiles
  *   split_k      1: phases with fewer tiles than half the CUs split K over
  *                several workgroups per tile (default); 0: never
+ *   k_stagger    S > 1: GEMM tile (tm, tn) of a settling phase sums its K
+ *                stages starting at stage (tm + tn) % S, so tiles sharing
+ *                operand rows do not all miss in L2 on the same rows at once;
+ *                0 or 1: every tile sums from stage 0.  Default 16 for 16-bit
+ *                models, 0 for fp32.  With S > 1 a row's bits depend on where
+ *                it falls in the batch (they stay the same run to run); with
+ *                0 a row's result is independent of the other rows.  At most 64.
  *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
  *                time every phase launch with HIP events (pcd_pc_profile_result) */
 int pcd_pc_set_option(pcd_model* model, const char* name, int value);

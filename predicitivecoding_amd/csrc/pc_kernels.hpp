@@ -143,6 +143,7 @@ struct PhaseArgs {
     const int* row_req;         // ragged: request of each row (nullable)
     const int* done_at;         // ragged: first step a request no longer runs
     int tile_order;             // TILE_INTERLEAVED or TILE_CONTIGUOUS (see phase_grid)
+    int k_stagger;              // > 1: K sweeps of tile (tm, tn) start (tm + tn) % k_stagger stages in
 };
 
 // How a phase's tiles are dealt over the XCDs.
@@ -445,6 +446,13 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     const int nk_all = P.K / KE;
     const int kb = split * nk_all / ks;             // this unit's stages [kb, kb + nk)
     const int nk = (split + 1) * nk_all / ks - kb;
+    // K stagger: tile (tm, tn) sweeps its stages starting at (tm + tn) % S and
+    // wrapping round.  The tiles of an XCD that share operand rows then ask for
+    // a row's next stage at different times: one takes the L2 miss and the
+    // others find the line resident, instead of all of them waiting on the same
+    // miss.  The sum over K is taken in that rotated order, so a row's result
+    // depends on the row tile it falls in (still the same run to run).
+    const int koff = (args.k_stagger > 1 && nk > 0) ? ((tm + tn) % args.k_stagger) % nk : 0;
     const char* Ag = (const char*)P.A + (size_t)row0 * P.lda * OPB + (size_t)kb * C::RB;
     const char* Bg = (const char*)P.B + (size_t)col0 * P.ldb * OPB + (size_t)kb * C::RB;
     const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
@@ -464,8 +472,10 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
     auto issue_stage = [&](int kt) PCD_INLINE {
         const uint32_t base = lds0 + (kt % C::NS) * C::stage_bytes + wave_u * C::QPW * 1024;
+        int kk = kt + koff;
+        if (kk >= nk) kk -= nk;
 #pragma unroll
-        for (int i = 0; i < C::QPW; ++i) lds_dma16(src[i] + (size_t)kt * C::RB, base + i * 1024);
+        for (int i = 0; i < C::QPW; ++i) lds_dma16(src[i] + (size_t)kk * C::RB, base + i * 1024);
     };
     // Fragments of K chunk c (32 bytes per row) of the stage in `slot`.
     const int half = lane >> 5, lr = lane & 31;

@@ -73,6 +73,58 @@ def test_every_tile_shape(oracle, dtype, tile):
     assert all(v < tol for v in errs.values()), errs
 
 
+@pytest.mark.parametrize("dtype,stagger", [("f32", 16), ("f32", 3), ("bf16", 0), ("bf16", 16), ("f16", 64)])
+@pytest.mark.parametrize("tile", [(64, 64), (256, 256)])
+def test_k_stagger_parity(oracle, dtype, stagger, tile):
+    # many row and column tiles, so the stage offsets (tm + tn) % S take many values
+    snap, W, b, P, x = build_case([300, 520, 260, 70], "gelu", 0.1, batch=600, seed=19, init="fanin")
+    top, st, en = run_gpu(snap, x, 6, dtype=dtype, states=True, energy=True,
+                          options={"tile": tile[0], "tile_n": tile[1], "k_stagger": stagger})
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 6, dtype=dtype, states=True, energy=True)
+    tol = 1e-4 if dtype == "f32" else 2e-3
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren),
+                states=max(max_rel(a, r) for a, r in zip(st, rst)))
+    _report(f"k_stagger={stagger}/{dtype}/tile{tile}", **errs)
+    assert all(v < tol for v in errs.values()), errs
+
+
+def test_k_stagger_changes_only_the_summation_order():
+    # the option is really applied (fp32 sums in another order differ in the
+    # last bits) and the default of a 16-bit model is on: setting the default
+    # value explicitly changes nothing
+    snap, _, _, _, x = build_case([300, 520, 260], "tanh", 0.1, batch=600, seed=20)
+    a, _, ea = run_gpu(snap, x, 5, energy=True, options={"tile": 64})
+    c, _, ec = run_gpu(snap, x, 5, energy=True, options={"tile": 64, "k_stagger": 16})
+    assert not np.array_equal(ea, ec)
+    assert max_rel(c, a) < 1e-5 and max_rel(ec, ea) < 1e-5
+    d, _, ed = run_gpu(snap, x, 5, dtype="bf16", energy=True, options={"tile": 64})
+    e, _, ee = run_gpu(snap, x, 5, dtype="bf16", energy=True, options={"tile": 64, "k_stagger": 16})
+    assert np.array_equal(d, e) and np.array_equal(ed, ee)
+
+
+def test_k_stagger_off_keeps_16bit_rows_independent():
+    snap, W, b, P, x = build_case([80, 300, 40], "tanh", 0.1, batch=400, seed=21)
+    perm = np.random.default_rng(1).permutation(400)
+    opts = {"tile": 64, "k_stagger": 0}
+    top, _, en = run_gpu(snap, x, 5, dtype="bf16", energy=True, options=opts)
+    ptop, _, pen = run_gpu(snap, x[perm], 5, dtype="bf16", energy=True, options=opts)
+    assert np.array_equal(top[perm], ptop) and np.array_equal(en[:, perm], pen)
+
+
+def test_k_stagger_option_values():
+    from predicitivecoding_amd import DeviceException, PcDeviceModel
+    snap, _, _, _, _ = build_case([16, 8], "tanh", 0.1, batch=2)
+    m = PcDeviceModel(snap, "bf16")
+    try:
+        for bad in (-1, 65):
+            with pytest.raises(DeviceException):
+                m.set_option("k_stagger", bad)
+        for ok in (0, 1, 2, 64):
+            m.set_option("k_stagger", ok)
+    finally:
+        m.close()
+
+
 def test_graph_and_eager_agree_bit_for_bit():
     snap, W, b, P, x = build_case([64, 128, 32], "tanh", 0.1, batch=50, seed=9)
     g_top, _, g_en = run_gpu(snap, x, 7, energy=True, options={"use_graph": 1})
