@@ -291,6 +291,10 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *                models, 0 for fp32.  With S > 1 a row's bits depend on where
  *                it falls in the batch (they stay the same run to run); with
  *                0 a row's result is independent of the other rows.  At most 64.
+ *   ragged_tiles 1: before each step of pcd_pc_relax_ragged, list the row tiles
+ *                that still hold a running row, and deal only those tiles over
+ *                the XCDs (default); 0: launch every tile, and let tiles whose
+ *                rows have all finished return at once.  Results are the same.
  *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
  *                time every phase launch with HIP events (pcd_pc_profile_result) */
 int pcd_pc_set_option(pcd_model* model, const char* name, int value);

@@ -106,6 +106,48 @@ __global__ void exit_kernel(const float* __restrict__ part, int ldp, int nslots,
     }
 }
 
+// Ragged: the row tiles of bm rows that hold a row still running at step t
+// (a row of request r runs while t < done_at[r]), listed in increasing order,
+// and their number.  One workgroup of kActTilesThreads threads; at most
+// kMaxActTiles row tiles.  Requests own the contiguous row ranges
+// [row_offsets[r], row_offsets[r + 1]).
+constexpr int kActTilesThreads = 1024;
+constexpr int kMaxActTiles = 16384;
+__global__ void __launch_bounds__(kActTilesThreads)
+active_tiles_kernel(const int* __restrict__ row_offsets, const int* __restrict__ done_at, int requests, int rows,
+                    int bm, int t, int* __restrict__ list, int* __restrict__ count) {
+    __shared__ unsigned char live[kMaxActTiles];
+    __shared__ int sums[kActTilesThreads];
+    const int tid = threadIdx.x;
+    const int ntiles = min((rows + bm - 1) / bm, kMaxActTiles);
+    for (int i = tid; i < ntiles; i += kActTilesThreads) live[i] = 0;
+    __syncthreads();
+    for (int r = tid; r < requests; r += kActTilesThreads) {
+        const int r0 = row_offsets[r], r1 = min(row_offsets[r + 1], rows);
+        if (r1 > r0 && t < done_at[r])
+            for (int i = r0 / bm; i <= (r1 - 1) / bm && i < ntiles; ++i) live[i] = 1;
+    }
+    __syncthreads();
+    // Thread tid owns the contiguous tiles [tid * per, (tid + 1) * per): count,
+    // scan the counts over the workgroup, then write the owned entries.
+    const int per = (ntiles + kActTilesThreads - 1) / kActTilesThreads;
+    const int lo = min(tid * per, ntiles), hi = min(lo + per, ntiles);
+    int mine = 0;
+    for (int i = lo; i < hi; ++i) mine += live[i];
+    sums[tid] = mine;
+    __syncthreads();
+    for (int d = 1; d < kActTilesThreads; d <<= 1) {
+        const int add = tid >= d ? sums[tid - d] : 0;
+        __syncthreads();
+        sums[tid] += add;
+        __syncthreads();
+    }
+    int at = sums[tid] - mine;
+    for (int i = lo; i < hi; ++i)
+        if (live[i]) list[at++] = i;
+    if (tid == kActTilesThreads - 1) count[0] = sums[tid];
+}
+
 // Row energies of a step from the per-slot partials when no update-phase
 // launch is there to reduce them (every free layer clamped).
 __global__ void energy_rows_kernel(const float* __restrict__ part, int ldp, int nslots, float* __restrict__ out,

@@ -144,6 +144,8 @@ struct PhaseArgs {
     const int* done_at;         // ragged: first step a request no longer runs
     int tile_order;             // TILE_INTERLEAVED or TILE_CONTIGUOUS (see phase_grid)
     int k_stagger;              // > 1: K sweeps of tile (tm, tn) start (tm + tn) % k_stagger stages in
+    const int* act_tm;          // ragged: row tiles with a row still running, increasing (nullable)
+    const int* act_count;       // ragged: their number
 };
 
 // How a phase's tiles are dealt over the XCDs.
@@ -367,12 +369,19 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     // TILE_CONTIGUOUS instead gives XCD x one contiguous eighth of the phase's
     // tiles taken in problem order (phases of many tiles per CU, where the
     // balance evens out by itself).
+    // A ragged phase with a list of the row tiles still running deals only
+    // those: problem q then has n_act x tiles_n x ksplit work units, and row
+    // tile index tm below counts along the list.
+    const int n_act = args.act_tm != nullptr ? __builtin_amdgcn_readfirstlane(gld(args.act_count)) : -1;
+    auto units_of = [&](int q) PCD_INLINE {
+        return n_act < 0 ? kprobs[q].tiles : n_act * kprobs[q].tiles_n * max(kprobs[q].ksplit, 1);
+    };
     const int x = blockIdx.x % kXcds;
     int i = blockIdx.x / kXcds, p = 0, local = -1;
     if (args.tile_order == TILE_INTERLEAVED) {
         for (; p < set.n; ++p) {
             int lo, cnt;
-            xcd_share(kprobs[p].tiles, x, lo, cnt);
+            xcd_share(units_of(p), x, lo, cnt);
             if (i < cnt) {
                 local = lo + i;
                 break;
@@ -381,17 +390,17 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
         }
     } else {
         int total = 0;
-        for (int q = 0; q < set.n; ++q) total += kprobs[q].tiles;
+        for (int q = 0; q < set.n; ++q) total += units_of(q);
         int lo, cnt;
         xcd_share(total, x, lo, cnt);
         if (i < cnt) {
             int t = lo + i;
             for (; p < set.n; ++p) {
-                if (t < kprobs[p].tiles) {
+                if (t < units_of(p)) {
                     local = t;
                     break;
                 }
-                t -= kprobs[p].tiles;
+                t -= units_of(p);
             }
         }
     }
@@ -404,15 +413,17 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     local /= ks;
     // Grouped order: runs of 8 row tiles share one column tile.
     const int G = 8;
+    const int rows_m = n_act < 0 ? P.tiles_m : n_act;
     int group = local / (G * P.tiles_n);
     int first_m = group * G;
-    int gsize = min(P.tiles_m - first_m, G);
+    int gsize = min(rows_m - first_m, G);
     int in_group = local - group * G * P.tiles_n;
-    const int tm = first_m + in_group % gsize;
+    const int tm_at = first_m + in_group % gsize;
+    const int tm = n_act < 0 ? tm_at : __builtin_amdgcn_readfirstlane(gld(args.act_tm + tm_at));
     const int tn = in_group / gsize;
     const int row0 = tm * BM, col0 = tn * BN;
 
-    if (args.row_req != nullptr) {
+    if (args.row_req != nullptr && n_act < 0) {
         // Any active row in the tile?  The flag borrows the first word of the
         // (not yet used) stage ring, which the full ring leaves no room beside.
         volatile int* flag = (volatile int*)smem;

@@ -237,6 +237,8 @@ struct Workspace {
     int slots_cap = 0;
     float* split_part = nullptr;       // split-K partial tiles, kSplitPartTiles x 128 x 128 fp32
     int* split_count = nullptr;        // split-K finished-range counters, zero between launches
+    int* act_tm = nullptr;             // ragged: row tiles still running at the current step [cap / 64]
+    int* act_count = nullptr;          // ragged: their number
     hipStream_t capture = nullptr;     // private stream used for graph capture
     std::vector<std::unique_ptr<Plan>> plans;
     std::vector<void*> owned;          // every hipMalloc'ed buffer
@@ -269,6 +271,7 @@ struct pcd_model {
     // options
     int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED, split_k = 1;
     int k_stagger = 0;                  // settling phases only (kKStagger16 for 16-bit operands)
+    int ragged_tiles = 1;               // ragged phases deal only the row tiles still running
     float prof_err_ms = 0.f, prof_upd_ms = 0.f;
     int prof_launches = 0;
     uint64_t clock = 0;
@@ -454,6 +457,8 @@ int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out
     if ((st = dev_alloc_zero(w->owned, (void**)&w->split_part, (size_t)split_part_tiles(m) * 128 * 128 * 4)))
         return st;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->split_count, (size_t)split_part_tiles(m) * 4))) return st;
+    if ((st = dev_alloc_zero(w->owned, (void**)&w->act_tm, (size_t)(need / 64) * 4))) return st;
+    if ((st = dev_alloc_zero(w->owned, (void**)&w->act_count, 4))) return st;
     HIP_TRY(hipStreamCreateWithFlags(&w->capture, hipStreamNonBlocking));
     *out = w;
     return PCD_SUCCESS;
@@ -635,10 +640,20 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
             if ((st = launch_phase(m->dtype, tile, EPI_FFG, ps, fa, s))) return st;
         }
     }
+    // Ragged: before each step, list the row tiles that still hold a running
+    // row; both phases of the step then deal only those over the XCDs.
+    const bool tile_list = r.row_req != nullptr && m->ragged_tiles && (batch + tile.m - 1) / tile.m <= kMaxActTiles;
     for (int t = 0; t < r.steps; ++t) {
         PhaseArgs a = args;
         a.t = t;
         a.energy_out = nullptr;
+        if (tile_list) {
+            hipLaunchKernelGGL(active_tiles_kernel, dim3(1), dim3(kActTilesThreads), 0, s, r.row_offsets,
+                               (const int*)r.done_at, r.requests, batch, tile.m, t, w->act_tm, w->act_count);
+            if ((st = from_hip(hipGetLastError(), "active_tiles_kernel launch"))) return st;
+            a.act_tm = w->act_tm;
+            a.act_count = w->act_count;
+        }
         hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
         if (timer) {
             HIP_TRY(hipEventCreate(&e0));
@@ -1228,7 +1243,8 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
         if (value != TILE_INTERLEAVED && value != TILE_CONTIGUOUS)
             return fail(PCD_INVALID_VALUE, "tile_order must be 0 (interleaved) or 1 (contiguous)");
         m->tile_order = value;
-    } else if (n == "k_stagger") {
+    } else if (n == "ragged_tiles") m->ragged_tiles = value ? 1 : 0;
+    else if (n == "k_stagger") {
         if (value < 0 || value > kMaxKStagger)
             return fail(PCD_INVALID_VALUE, "k_stagger must be 0 (off) to %d", kMaxKStagger);
         m->k_stagger = value;

@@ -205,6 +205,43 @@ def test_ragged_requests_with_exit(oracle):
         m.close()
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("tile", [64, 128, 256])
+def test_ragged_tile_list_matches_full_grid(oracle, dtype, tile):
+    # Dealing only the row tiles still running (ragged_tiles = 1, the default)
+    # computes every tile exactly as the full grid does: identical bits.
+    from predicitivecoding_amd import PcDeviceModel
+    sizes = [96, 200, 130, 24]
+    snap, W, b, P, _ = build_case(sizes, "tanh", 0.1, seed=23, init="fanin")
+    rng = np.random.default_rng(4)
+    counts = rng.integers(1, 160, 40)
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    x = (rng.standard_normal((offs[-1], sizes[0])) * 0.5).astype(np.float32)
+    steps = rng.integers(2, 30, len(counts)).astype(np.int32)
+    out = {}
+    m = PcDeviceModel(snap, dtype)
+    try:
+        m.set_option("tile", tile)
+        for on in (1, 0):
+            m.set_option("ragged_tiles", on)
+            out[on] = [m.relax_ragged(x, offs, steps, "none"), m.relax_ragged(x, offs, steps, "absolute", 6.0)]
+    finally:
+        m.close()
+    for a, c in zip(out[1], out[0]):
+        for u, v in zip(a, c):
+            assert np.array_equal(u, v)
+    used, fe, top = out[1][1]
+    assert np.any(used < steps), "the exit rule never fired"
+    rused, rfe, rtop = oracle.ragged_relax(sizes, "tanh", 0.1, W, b, P, x, offs, steps, "absolute", 6.0,
+                                           round_mode={"f32": "none", "bf16": "bf16"}[dtype])
+    tol = 1e-4 if dtype == "f32" else 2e-3
+    decided = np.array_equal(used, rused)
+    _report(f"ragged list/{dtype}/tile{tile}", top=max_rel(top, rtop), energy=max_rel(fe, rfe),
+            exits_equal=float(decided))
+    if dtype == "f32":
+        assert decided and max_rel(top, rtop) < tol and max_rel(fe, rfe) < tol
+
+
 def test_gemm_entry_points():
     from predicitivecoding_amd import DeviceTensor, TensorOps
     from predicitivecoding_amd.gemm import HipGemmProvider
