@@ -86,7 +86,7 @@ __global__ void exit_kernel(const float* __restrict__ part, int ldp, int nslots,
     const int r0 = row_offsets[r], r1 = row_offsets[r + 1];
     float s = 0.f;
     for (int row = r0 + threadIdx.x; row < r1; row += blockDim.x)
-        for (int k = 0; k < nslots; ++k) s += part[(size_t)k * ldp + row];
+        s += sum_slots(part, ldp, nslots, row);
     __shared__ float red[256];
     red[threadIdx.x] = s;
     __syncthreads();
@@ -153,9 +153,7 @@ active_tiles_kernel(const int* __restrict__ row_offsets, const int* __restrict__
 __global__ void energy_rows_kernel(const float* __restrict__ part, int ldp, int nslots, float* __restrict__ out,
                                    int rows) {
     for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
-        float s = 0.f;
-        for (int k = 0; k < nslots; ++k) s += part[(size_t)k * ldp + r];
-        out[r] = s;
+        out[r] = sum_slots(part, ldp, nslots, r);
     }
 }
 
