@@ -279,7 +279,9 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
 /* Relaxation options (no counterpart in the reference; tuning and profiling
  * hooks for the host wrappers and the benchmark):
  *   use_graph    capture the T-step loop in a hipGraph (default 1)
- *   tile, tile_n force a GEMM tile (0 = automatic choice)
+ *   tile, tile_n force a GEMM tile (0 = automatic choice): tile sets rows and
+ *                columns, tile_n then the columns; supported 64 x 64,
+ *                64 x 128, 64 x 256, 128 x 128, 256 x 128, 256 x 256
  *   tile_order   0: every XCD runs an eighth of each problem's tiles (default);
  *                1: every XCD runs one contiguous eighth of the phase's tiles
  *   split_k      1: phases with fewer tiles than half the CUs split K over

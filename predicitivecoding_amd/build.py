@@ -20,7 +20,7 @@ HOST_SOURCE = os.path.join(CSRC, "pcdevice.hip")
 INST_SOURCE = os.path.join(CSRC, "phase_inst.hip")
 
 OPS = {"f32": 0, "bf16": 1, "f16": 2}
-TILES = [(64, 64), (128, 128), (256, 128), (256, 256)]
+TILES = [(64, 64), (64, 128), (64, 256), (128, 128), (256, 128), (256, 256)]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -62,7 +62,9 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> str:
             if verbose and out.strip():
                 print(out)
         tmp = LIB + ".tmp"
-        rc, out = _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC",
+        # -z defs: a tile the host dispatches but no unit instantiates fails here,
+        # not when the library is loaded
+        rc, out = _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-z,defs",
                         *[os.path.join(tmpdir, obj) for _, _, obj in units], "-o", tmp])
         if rc != 0:
             raise RuntimeError(f"link failed ({rc}):\n{out}")

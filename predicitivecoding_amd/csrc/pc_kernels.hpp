@@ -305,6 +305,9 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
 #ifndef PCD_OCC_SMALL
 #define PCD_OCC_SMALL 2
 #endif
+#ifndef PCD_SMALL_NS
+#define PCD_SMALL_NS 4
+#endif
 template <int BM, int BN> struct TileCfg {
     // 256 x 256 runs 8 waves (2 x 4 of 128 x 64: two waves per SIMD share the
     // MFMA pipe) over 128-byte K stages, double buffered (128 KB of LDS, one
@@ -320,7 +323,7 @@ template <int BM, int BN> struct TileCfg {
     static constexpr int UNITS = RB / 16;                  // 16-byte units per row
     static constexpr int NC = RB / 32;                     // 32-byte MFMA chunks per stage
     static constexpr int stage_bytes = (BM + BN) * RB;
-    static constexpr int NS = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : (BM == 256 && BN == 128) ? 3 : 4;   // stages in the LDS ring
+    static constexpr int NS = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : (BM + BN >= 320) ? 3 : PCD_SMALL_NS;   // stages in the LDS ring
     static constexpr int D = NS - 1;                       // prefetch distance (stages)
     static constexpr int OCC = BIG ? 1 : PCD_OCC_SMALL;    // workgroups per CU the registers are sized for
     static constexpr int ROWS_PER_LOAD = 64 * 16 / RB;     // rows one wave-wide 16-byte-per-lane load fills
@@ -328,7 +331,7 @@ template <int BM, int BN> struct TileCfg {
     static_assert(FM >= 1 && FN >= 1 && QPW >= 1, "tile too small");
     static_assert((BM + BN) % (NWAVES * ROWS_PER_LOAD) == 0, "stage rows must split evenly over the waves");
     static_assert(NC % 2 == 0, "fragment buffers alternate within a stage");
-    static_assert(D >= 1 && D <= 4, "stage_ready handles prefetch distances 1 to 4");
+    static_assert(D >= 1 && D * QPW < 64, "stage_ready waits on at most 63 loads");
     static_assert(NS * stage_bytes <= 160 * 1024, "LDS ring exceeds the 160 KB of a CU");
 };
 
@@ -544,22 +547,11 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     // Wait until stage `next` has landed for this wave, given how many later
     // stages are still in flight, then make it visible to all waves.
     auto stage_ready = [&](int next) PCD_INLINE {
-        const int later = min(C::D - 1, nk - 1 - next);
-        if constexpr (C::D >= 4) {
-            if (later >= 3) wait_vmcnt<3 * C::QPW>();
-            else if (later == 2) wait_vmcnt<2 * C::QPW>();
-            else if (later == 1) wait_vmcnt<C::QPW>();
-            else wait_vmcnt<0>();
-        } else if constexpr (C::D >= 3) {
-            if (later >= 2) wait_vmcnt<2 * C::QPW>();
-            else if (later == 1) wait_vmcnt<C::QPW>();
-            else wait_vmcnt<0>();
-        } else if constexpr (C::D == 2) {
-            if (later >= 1) wait_vmcnt<C::QPW>();
-            else wait_vmcnt<0>();
-        } else {
-            wait_vmcnt<0>();
-        }
+        const int later = min(C::D - 1, nk - 1 - next);   // 0 .. D-1
+        static_for<0, C::D>([&](auto Kc) PCD_INLINE {
+            constexpr int k = decltype(Kc)::value;
+            if (later == k) wait_vmcnt<k * C::QPW>();
+        });
         __syncthreads();
     };
     constexpr int NC = C::NC;

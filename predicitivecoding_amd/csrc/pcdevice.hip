@@ -156,13 +156,15 @@ struct Tile {
     int m, n;
 };
 bool tile_supported(Tile t) {
-    return (t.m == 64 && t.n == 64) || (t.m == 128 && t.n == 128) || (t.m == 256 && t.n == 128) ||
-           (t.m == 256 && t.n == 256);
+    return (t.m == 64 && (t.n == 64 || t.n == 128 || t.n == 256)) || (t.m == 128 && t.n == 128) ||
+           (t.m == 256 && t.n == 128) || (t.m == 256 && t.n == 256);
 }
 
 template <typename OP>
 int launch_op(Tile tile, int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
     if (tile.m == 64 && tile.n == 64) return launch_tile<OP, 64, 64>(epi, set, args, grid, s);
+    if (tile.m == 64 && tile.n == 128) return launch_tile<OP, 64, 128>(epi, set, args, grid, s);
+    if (tile.m == 64 && tile.n == 256) return launch_tile<OP, 64, 256>(epi, set, args, grid, s);
     if (tile.m == 128 && tile.n == 128) return launch_tile<OP, 128, 128>(epi, set, args, grid, s);
     if (tile.m == 256 && tile.n == 128) return launch_tile<OP, 256, 128>(epi, set, args, grid, s);
     if (tile.m == 256 && tile.n == 256) return launch_tile<OP, 256, 256>(epi, set, args, grid, s);
@@ -315,6 +317,9 @@ long error_phase_tiles(const pcd_model* m, int batch, Tile t) {
 // operands with every layer at least 1024 wide.
 Tile choose_tile(const pcd_model* m, int batch) {
     if (m->tile_m > 0) return Tile{m->tile_m, m->tile_n};
+    // A batch that fits one 64-row tile: any taller tile is mostly padding rows
+    // (its MFMAs and its state loads wasted), and the phases stream weights.
+    if (batch <= 64) return Tile{64, 64};
     const long want = 2L * m->cus;
     if (m->dtype != PCD_F32) {
         bool wide = true;
@@ -330,6 +335,8 @@ int slots_per_tile_n(Tile t) {
     if (t.m == 256 && t.n == 256) return energy_slots_per_tile_n<256, 256>();
     if (t.m == 256 && t.n == 128) return energy_slots_per_tile_n<256, 128>();
     if (t.m == 128 && t.n == 128) return energy_slots_per_tile_n<128, 128>();
+    if (t.m == 64 && t.n == 128) return energy_slots_per_tile_n<64, 128>();
+    if (t.m == 64 && t.n == 256) return energy_slots_per_tile_n<64, 256>();
     return energy_slots_per_tile_n<64, 64>();
 }
 
@@ -342,7 +349,7 @@ int energy_slots(const pcd_model* m, Tile tile) {
 
 // The most slots any supported tile needs (sizes the workspace once).
 int max_energy_slots(const pcd_model* m) {
-    const Tile tiles[] = {{64, 64}, {128, 128}, {256, 128}, {256, 256}};
+    const Tile tiles[] = {{64, 64}, {64, 128}, {64, 256}, {128, 128}, {256, 128}, {256, 256}};
     int slots = 0;
     for (Tile t : tiles) slots = std::max(slots, energy_slots(m, t));
     return slots;

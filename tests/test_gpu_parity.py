@@ -62,7 +62,7 @@ def test_16bit_operands(oracle, dtype, act):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("tile", [(64, 64), (128, 128), (256, 128), (256, 256)])
+@pytest.mark.parametrize("tile", [(64, 64), (64, 128), (64, 256), (128, 128), (256, 128), (256, 256)])
 def test_every_tile_shape(oracle, dtype, tile):
     snap, W, b, P, x = build_case([300, 260, 200], "tanh", 0.1, batch=300, seed=7, bias_scale=0.1)
     top, _, en = run_gpu(snap, x, 6, dtype=dtype, energy=True, options={"tile": tile[0], "tile_n": tile[1]})
