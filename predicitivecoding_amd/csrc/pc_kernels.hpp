@@ -308,22 +308,32 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
 #ifndef PCD_SMALL_NS
 #define PCD_SMALL_NS 4
 #endif
-template <int BM, int BN> struct TileCfg {
+#ifndef PCD_SMALL_RB
+#define PCD_SMALL_RB 64
+#endif
+#ifndef PCD_SMALL_RB16
+#define PCD_SMALL_RB16 128
+#endif
+template <int BM, int BN, int OPB = 4> struct TileCfg {
     // 256 x 256 runs 8 waves (2 x 4 of 128 x 64: two waves per SIMD share the
     // MFMA pipe) over 128-byte K stages, double buffered (128 KB of LDS, one
-    // workgroup per CU).  The other tiles run 4 waves (2 x 2) over 64-byte
-    // stages; 256 x 128 keeps 3 stages (72 KB) so two workgroups fit a CU.
+    // workgroup per CU).  The other tiles run 4 waves (2 x 2) with rings of at
+    // most 80 KB, so two workgroups fit a CU.  Their stages are 64 bytes per
+    // row, except 64-row tiles on 16-bit operands: 128 bytes, one whole cache
+    // line of every weight row per stage, which is what streams best from HBM
+    // when the batch is small (the weights dominate the traffic).
     static constexpr bool BIG = BM == 256 && BN == 256;
     static constexpr int WM = 2, WN = BIG ? 4 : 2;
     static constexpr int NWAVES = WM * WN, NT = 64 * NWAVES;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
     static constexpr bool MID = BM == 128 && BN == 128;
-    static constexpr int RB = BIG ? PCD_BIG_RB : MID ? PCD_MID_RB : 64;       // K bytes per row per stage
+    static constexpr int RB = BIG ? PCD_BIG_RB : MID ? PCD_MID_RB : (BM == 64 && OPB == 2) ? PCD_SMALL_RB16 : PCD_SMALL_RB;   // K bytes per row per stage
     static constexpr int UNITS = RB / 16;                  // 16-byte units per row
     static constexpr int NC = RB / 32;                     // 32-byte MFMA chunks per stage
     static constexpr int stage_bytes = (BM + BN) * RB;
-    static constexpr int NS = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : (BM + BN >= 320) ? 3 : PCD_SMALL_NS;   // stages in the LDS ring
+    static constexpr int NS_WANT = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : (BM + BN >= 320) ? 3 : PCD_SMALL_NS;
+    static constexpr int NS = BIG ? NS_WANT : (NS_WANT * stage_bytes <= 80 * 1024 ? NS_WANT : 80 * 1024 / stage_bytes);   // stages in the LDS ring
     static constexpr int D = NS - 1;                       // prefetch distance (stages)
     static constexpr int OCC = BIG ? 1 : PCD_OCC_SMALL;    // workgroups per CU the registers are sized for
     static constexpr int ROWS_PER_LOAD = 64 * 16 / RB;     // rows one wave-wide 16-byte-per-lane load fills
@@ -333,6 +343,7 @@ template <int BM, int BN> struct TileCfg {
     static_assert(NC % 2 == 0, "fragment buffers alternate within a stage");
     static_assert(D >= 1 && D * QPW < 64, "stage_ready waits on at most 63 loads");
     static_assert(NS * stage_bytes <= 160 * 1024, "LDS ring exceeds the 160 KB of a CU");
+    static_assert(64 % (RB / OPB) == 0, "K is padded to 64 elements: a stage's K must divide it");
 };
 
 // Energy partial slots one tile column owns (one per wave column).
@@ -358,8 +369,8 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 template <typename OP, int BM, int BN, int EPI>
 __global__ void __launch_bounds__((TileCfg<BM, BN>::NT), (TileCfg<BM, BN>::OCC))
 phase_kernel(const ProblemSet set, const PhaseArgs args) {
-    using C = TileCfg<BM, BN>;
     constexpr int OPB = OpTraits<OP>::bytes;
+    using C = TileCfg<BM, BN, OPB>;
     __shared__ __attribute__((aligned(16))) char smem[C::NS * C::stage_bytes];
 
     const int tid = threadIdx.x;

@@ -376,10 +376,17 @@ int split_factor(int cus, int split_k, long tiles, Tile tile) {
 }
 
 // K elements of one LDS stage of `tile` for an operand type.
+template <int OPB> int stage_rb(Tile t) {
+    if (t.m == 64 && t.n == 64) return TileCfg<64, 64, OPB>::RB;
+    if (t.m == 64 && t.n == 128) return TileCfg<64, 128, OPB>::RB;
+    if (t.m == 64 && t.n == 256) return TileCfg<64, 256, OPB>::RB;
+    if (t.m == 128 && t.n == 128) return TileCfg<128, 128, OPB>::RB;
+    if (t.m == 256 && t.n == 128) return TileCfg<256, 128, OPB>::RB;
+    return TileCfg<256, 256, OPB>::RB;
+}
+
 int stage_k(int dtype, Tile tile) {
-    int rb = 64;
-    if (tile.m == 128 && tile.n == 128) rb = TileCfg<128, 128>::RB;
-    else if (tile.m == 256 && tile.n == 256) rb = TileCfg<256, 256>::RB;
+    const int rb = dtype == PCD_F32 ? stage_rb<4>(tile) : stage_rb<2>(tile);
     return rb / op_bytes(dtype);
 }
 
