@@ -162,7 +162,7 @@ def cpu_baseline(cfg, W, b, x_host, budget_s=10.0):
 
 
 def traffic_from_profiles(workload, kernel):
-    """HBM bytes per launch of `kernel` ("error_phase" / "update_phase") from
+    """HBM bytes per launch of `kernel` ("error_phase", "update_phase", "plain") from
     the committed PMC summary profiles/traffic_<workload>.json (written by
     --traffic-from), or None when it has not been measured."""
     path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
@@ -215,17 +215,20 @@ def _mean_counter(rows, counter, name_filter):
         key = r.get("Dispatch_Id") or r.get("Correlation_Id")
         per_dispatch[key] = per_dispatch.get(key, 0.0) + float(r["Counter_Value"])
     if not per_dispatch:
-        raise SystemExit(f"no {counter} rows for the requested kernel")
+        return None, 0
     return sum(per_dispatch.values()) / len(per_dispatch), len(per_dispatch)
 
 
-def traffic_from_pmc(workload, fetch_dir, write_dir, calib_fetch_dir, calib_write_dir, command):
-    """Writes profiles/traffic_<workload>.json: HBM bytes per launch of each
-    phase kernel from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each
-    scaled by what the same counter reads for the calibration copy."""
+def traffic_from_pmc(workload, fetch_dir, write_dir, calib_fetch_dir, calib_write_dir, command, out_path=None):
+    """Writes profiles/traffic_<workload>.json (or out_path): HBM bytes per
+    launch of each phase kernel from FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by what the same counter reads for the calibration
+    copy."""
     is_copy = lambda n: "MulFunctor" in n
     cf, _ = _mean_counter(_pmc_rows(calib_fetch_dir), "FETCH_SIZE", is_copy)
     cw, _ = _mean_counter(_pmc_rows(calib_write_dir), "WRITE_SIZE", is_copy)
+    if cf is None or cw is None:
+        raise SystemExit("no calibration copy dispatches in the calibration runs")
     f_fetch = cf * 1024.0 / COPY_CALIB_BYTES
     f_write = cw * 1024.0 / COPY_CALIB_BYTES
     fr, wr = _pmc_rows(fetch_dir), _pmc_rows(write_dir)
@@ -233,17 +236,19 @@ def traffic_from_pmc(workload, fetch_dir, write_dir, calib_fetch_dir, calib_writ
            "calibration": {"bytes": COPY_CALIB_BYTES, "fetch_kib": cf, "write_kib": cw,
                            "fetch_factor": f_fetch, "write_factor": f_write},
            "kernels": {}}
-    for name, tag in (("error_phase", ", 0>"), ("update_phase", ", 1>")):
+    for name, tag in (("error_phase", ", 0>"), ("update_phase", ", 1>"), ("plain", ", 3>")):
         sel = lambda n, tag=tag: "phase_kernel" in n and n.rstrip().endswith(tag + "(pcd::ProblemSet, pcd::PhaseArgs)")
         fk, nf = _mean_counter(fr, "FETCH_SIZE", sel)
         wk, nw = _mean_counter(wr, "WRITE_SIZE", sel)
+        if fk is None or wk is None:
+            continue  # this workload launches no such kernel
         fetch_b = fk * 1024.0 / f_fetch
         write_b = wk * 1024.0 / f_write
         out["kernels"][name] = {"fetch_kib": fk, "write_kib": wk, "dispatches": [nf, nw],
                                 "fetch_bytes": fetch_b, "write_bytes": write_b,
                                 "bytes_per_launch": fetch_b + write_b}
-    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
-    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    path = out_path or os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    os.makedirs(os.path.dirname(path), exist_ok=True)
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
     print(json.dumps(out, indent=1))
@@ -505,7 +510,8 @@ def bench_gemm(args, cfg):
         "config": {"workload": f"gemm: pcd_gemm_bf16 {m} x {k} x {n}, B given transposed (K-contiguous)",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[cfg["dtype"]] / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK[cfg["dtype"]], "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK[cfg["dtype"]],
+                     "traffic": traffic_from_profiles("gemm", "plain"),
                      "kernel": "phase_kernel EPI_PLAIN", "kernel_ms": kms},
         "cpu_baseline": cpu,
     }
