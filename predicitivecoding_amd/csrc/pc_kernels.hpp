@@ -290,6 +290,10 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
     return unit ^ ((row / (256 / RB)) % (RB / 16));
 }
 
+// Build-time tile parameters (K bytes per row per stage: *_RB; LDS ring
+// stages: *_NS; workgroups per CU the registers are sized for: OCC).  The
+// defaults are the fastest measured on MI355X for the settling phases and the
+// GEMM provider; a -D on the compiler line overrides one to measure another.
 #ifndef PCD_BIG_RB
 #define PCD_BIG_RB 128
 #endif
