@@ -204,9 +204,8 @@ __device__ __forceinline__ float act_f(int act, float x) {
 
 // Round-to-nearest-even fp32 -> bf16 with NaN kept NaN (TensorUtils.cs:386-395).
 __device__ __forceinline__ uint16_t to_bf16(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
-    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+    __bf16 h = (__bf16)x;  // v_cvt_pk_bf16_f32, round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
 }
 __device__ __forceinline__ uint16_t to_f16(float x) {
     _Float16 h = (_Float16)x;  // v_cvt_f16_f32, round to nearest even
@@ -705,6 +704,18 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     // Row of register r of a block in row-block i: 8*(r/4) + 4*half + r%4.
     auto row_of = [&](int i, int r) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
     auto col_of = [&](int j) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + lr; };
+    // In the update and plain epilogues a full tile (every row and column
+    // valid, no ragged rows) takes a path with no per-element test: each
+    // element's offset is the block's base plus a per-register row step, and
+    // the per-problem choices (folded update or not, the C term) are made once
+    // per block.  Partial and ragged tiles test every element.  The error
+    // epilogue tests every element on every tile: without the tests' branches
+    // the compiler hoists its loads and addresses until the 256 x 256 tile
+    // spills registers.
+    const int ldo = P.ldo;
+    auto rstep = [&](int r) PCD_INLINE { return (size_t)(8 * (r >> 2) + (r & 3)) * ldo; };
+    auto base_of = [&](int i, int j) PCD_INLINE { return (size_t)row_of(i, 0) * ldo + col_of(j); };
+    const bool full = row0 + BM <= P.M && col0 + BN <= P.N && args.row_req == nullptr;
     if constexpr (EPI == EPI_ERROR) {
         // On the 256 x 256 tile (the large 16-bit models), one copy of the
         // epilogue per activation, chosen once per tile: the per-element
@@ -728,7 +739,7 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                 static_for<0, 16>([&](auto R) PCD_INLINE {
                     constexpr int r = decltype(R)::value;
                     const int row = row_of(i, r);
-                    mv[b % PD][r] = (col < P.N && row < P.M) ? gld(P.mlow + (size_t)row * P.ldo + col) : 0.f;
+                    mv[b % PD][r] = (col < P.N && row < P.M) ? gld(P.mlow + (size_t)row * ldo + col) : 0.f;
                 });
             };
             static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
@@ -742,7 +753,7 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                     constexpr int r = decltype(R)::value;
                     const int row = row_of(i, r);
                     if (cok && row < P.M && row_active(args, row)) {
-                        const size_t idx = (size_t)row * P.ldo + col;
+                        const size_t idx = (size_t)row * ldo + col;
                         const float pre = acc[i][j][r] + bj;
                         float y, dy;
                         act_eval(ACT >= 0 ? ACT : args.act, pre, y, dy);
@@ -803,47 +814,86 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
         // lambda sign M_l) having been written by the error phase; the top
         // layer (E = 0) reads M_l itself: M_l -= eta (lambda sign M_l - G).
         // The operand of the next PD blocks is in flight while a block computes.
-        constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
-        const float eta = args.eta, lam = args.act_reg;
-        const bool folded = P.eself != nullptr;
-        const float* src = folded ? P.eself : P.m;
-        float xv[PD][16];
-        auto load_block = [&](auto Bc) PCD_INLINE {
-            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
-            const int col = col_of(j);
-            static_for<0, 16>([&](auto R) PCD_INLINE {
-                constexpr int r = decltype(R)::value;
-                const int row = row_of(i, r);
-                xv[b % PD][r] = (col < P.N && row < P.M) ? gld(src + (size_t)row * P.ldo + col) : 0.f;
-            });
-        };
-        static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
-        static_for<0, NB>([&](auto Bc) PCD_INLINE {
-            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
-            const int col = col_of(j);
-            if (col < P.N) {
-                static_for<0, 16>([&](auto R) PCD_INLINE {
-                    constexpr int r = decltype(R)::value;
-                    const int row = row_of(i, r);
-                    if (row < P.M && row_active(args, row)) {
-                        const size_t idx = (size_t)row * P.ldo + col;
-                        const float x = xv[b % PD][r];
-                        float m;
-                        if (folded) {
-                            m = x + eta * acc[i][j][r];
-                        } else {
+        auto epilogue = [&](auto FullC) PCD_INLINE {
+            constexpr bool FULL = decltype(FullC)::value;
+            constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
+            const float eta = args.eta, lam = args.act_reg;
+            const bool folded = P.eself != nullptr;
+            const float* src = folded ? P.eself : P.m;
+            float xv[PD][16];
+            auto load_block = [&](auto Bc) PCD_INLINE {
+                constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+                if constexpr (FULL) {
+                    static_for<0, 16>([&](auto R) PCD_INLINE {
+                        constexpr int r = decltype(R)::value;
+                        xv[b % PD][r] = gld(src + base_of(i, j) + rstep(r));
+                    });
+                } else {
+                    const int col = col_of(j);
+                    static_for<0, 16>([&](auto R) PCD_INLINE {
+                        constexpr int r = decltype(R)::value;
+                        const int row = row_of(i, r);
+                        xv[b % PD][r] = (col < P.N && row < P.M) ? gld(src + (size_t)row * ldo + col) : 0.f;
+                    });
+                }
+            };
+            static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
+            static_for<0, NB>([&](auto Bc) PCD_INLINE {
+                constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+                if constexpr (FULL) {
+                    float mn[16];
+                    if (folded) {
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            mn[r] = xv[b % PD][r] + eta * acc[i][j][r];
+                        });
+                    } else {
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            const float x = xv[b % PD][r];
                             float grad = -acc[i][j][r];
                             if (lam > 0.f) grad += lam * (x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f));
-                            m = x - eta * grad;
-                        }
-                        gst(P.m + idx, m);
-                        if (P.mop) OpTraits<OP>::store(P.mop, idx, m);
+                            mn[r] = x - eta * grad;
+                        });
                     }
-                });
-            }
-            if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
-            __builtin_amdgcn_sched_barrier(0);
-        });
+                    static_for<0, 16>([&](auto R) PCD_INLINE {
+                        constexpr int r = decltype(R)::value;
+                        gst(P.m + base_of(i, j) + rstep(r), mn[r]);
+                    });
+                    if (P.mop)
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            OpTraits<OP>::store(P.mop, base_of(i, j) + rstep(r), mn[r]);
+                        });
+                } else {
+                    const int col = col_of(j);
+                    if (col < P.N) {
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            const int row = row_of(i, r);
+                            if (row < P.M && row_active(args, row)) {
+                                const size_t idx = (size_t)row * ldo + col;
+                                const float x = xv[b % PD][r];
+                                float m;
+                                if (folded) {
+                                    m = x + eta * acc[i][j][r];
+                                } else {
+                                    float grad = -acc[i][j][r];
+                                    if (lam > 0.f) grad += lam * (x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f));
+                                    m = x - eta * grad;
+                                }
+                                gst(P.m + idx, m);
+                                if (P.mop) OpTraits<OP>::store(P.mop, idx, m);
+                            }
+                        });
+                    }
+                }
+                if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        };
+        if (full) epilogue(std::true_type{});
+        else epilogue(std::false_type{});
     } else if constexpr (EPI == EPI_FFG) {
         static_for<0, C::FM>([&](auto I) PCD_INLINE {
             constexpr int i = decltype(I)::value;
@@ -857,7 +907,7 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                         constexpr int r = decltype(R)::value;
                         const int row = row_of(i, r);
                         if (row < P.M) {
-                            const size_t idx = (size_t)row * P.ldo + col;
+                            const size_t idx = (size_t)row * ldo + col;
                             const float y = act_f(args.act, acc[i][j][r] + bj);
                             gst(P.m + idx, y);
                             if (P.dout) OpTraits<OP>::store(P.dout, idx, y);
@@ -867,23 +917,43 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
             });
         });
     } else {  // EPI_PLAIN: C = alpha acc + beta C
+        const float alpha = args.alpha, beta = args.beta;
         static_for<0, C::FM>([&](auto I) PCD_INLINE {
             constexpr int i = decltype(I)::value;
             static_for<0, C::FN>([&](auto J) PCD_INLINE {
                 constexpr int j = decltype(J)::value;
                 __builtin_amdgcn_sched_barrier(0);  // keep each block's epilogue to itself
-                const int col = col_of(j);
-                if (col < P.N) {
-                    static_for<0, 16>([&](auto R) PCD_INLINE {
-                        constexpr int r = decltype(R)::value;
-                        const int row = row_of(i, r);
-                        if (row < P.M) {
-                            const size_t idx = (size_t)row * P.ldo + col;
-                            float v = args.alpha * acc[i][j][r];
-                            if (args.beta != 0.f) v += args.beta * gld(P.m + idx);
-                            gst(P.m + idx, v);
-                        }
-                    });
+                if (full) {
+                    if (beta != 0.f) {
+                        float cv[16];
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            cv[r] = gld(P.m + base_of(i, j) + rstep(r));
+                        });
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            gst(P.m + base_of(i, j) + rstep(r), alpha * acc[i][j][r] + beta * cv[r]);
+                        });
+                    } else {
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            gst(P.m + base_of(i, j) + rstep(r), alpha * acc[i][j][r]);
+                        });
+                    }
+                } else {
+                    const int col = col_of(j);
+                    if (col < P.N) {
+                        static_for<0, 16>([&](auto R) PCD_INLINE {
+                            constexpr int r = decltype(R)::value;
+                            const int row = row_of(i, r);
+                            if (row < P.M) {
+                                const size_t idx = (size_t)row * ldo + col;
+                                float v = alpha * acc[i][j][r];
+                                if (beta != 0.f) v += beta * gld(P.m + idx);
+                                gst(P.m + idx, v);
+                            }
+                        });
+                    }
                 }
             });
         });
