@@ -208,6 +208,28 @@ def test_learn_step_16bit_masters(oracle, dtype):
     assert all(v < 2e-3 for v in errs.values()), errs
 
 
+@pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("bf16", 2e-3)])
+def test_learn_step_c2_network(oracle, dtype, tol):
+    # one learning step on BASELINE configs[1]'s network (1024-1024-1024-1024-256 tanh, eta 0.05)
+    # with a batch of 64 labelled rows and T = 20, against the oracle's Learn (same operand rounding)
+    sizes = [1024, 1024, 1024, 1024, 256]
+    snap, W, b, P, x = build_case(sizes, "tanh", 0.05, batch=64, seed=25)
+    y = _one_hot(np.arange(64) % 256, 256)
+    m = _model(snap, dtype)
+    try:
+        en = m.learn(x, y, 20, 0.01, 0.001)
+        gw, gb = m.get_weights()
+    finally:
+        m.close()
+    rw, rb, ren = oracle.learn(sizes, "tanh", 0.05, W, b, P, x, y, 20, 0.01, weight_decay=0.001,
+                               round_mode=ROUND[dtype])
+    errs = dict(weights=max(max_rel(a, r) for a, r in zip(gw, rw)), biases=max(max_rel(a, r) for a, r in zip(gb, rb)),
+                energy=max_rel(en, ren),
+                update=max(max_rel(a - w0, r - w0) for a, r, w0 in zip(gw, rw, W)))
+    _report(f"learn c2 network {dtype}", **errs)
+    assert all(v < tol for v in errs.values()), errs
+
+
 def test_learn_mixed_predicts_like_float(oracle):
     # NetworkTests' mixed-precision contract: the bf16 model trained with
     # LearnMixed's scheme classifies the two patterns like the fp32 network
