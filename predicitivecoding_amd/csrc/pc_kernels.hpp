@@ -80,6 +80,14 @@ __device__ __forceinline__ float gld(const float* p) { return *(const gfloat*)p;
 __device__ __forceinline__ int gld(const int* p) { return *(const gint*)p; }
 __device__ __forceinline__ void gst(float* p, float v) { *(gfloat*)p = v; }
 __device__ __forceinline__ void gst(uint16_t* p, uint16_t v) { *(gu16*)p = v; }
+// Four consecutive elements in one access (16 bytes of fp32, 8 of a 16-bit type).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) f32x4 gf32x4;
+typedef __attribute__((address_space(1))) u32x2 gu32x2;
+__device__ __forceinline__ f32x4 gld4(const float* p) { return *(const gf32x4*)p; }
+__device__ __forceinline__ void gst4(float* p, f32x4 v) { *(gf32x4*)p = v; }
+__device__ __forceinline__ void gst4(uint16_t* p, u32x2 v) { *(gu32x2*)p = v; }
 
 // bf16 and fp16 are carried as raw 16-bit patterns.
 struct bf16_t { uint16_t v; };
@@ -212,15 +220,23 @@ __device__ __forceinline__ uint16_t to_f16(float x) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// store4 writes elements idx .. idx+3 (idx a multiple of 4) in one access;
+// the conversions round to nearest even, as the one-element stores do.
 template <typename OP> struct OpTraits;
 template <> struct OpTraits<float> {
     static constexpr int bytes = 4;
     __device__ static void store(void* base, size_t idx, float v) { gst((float*)base + idx, v); }
+    __device__ static void store4(void* base, size_t idx, f32x4 v) { gst4((float*)base + idx, v); }
     __device__ static float load(const void* base, size_t idx) { return ((const float*)base)[idx]; }
 };
 template <> struct OpTraits<bf16_t> {
     static constexpr int bytes = 2;
     __device__ static void store(void* base, size_t idx, float v) { gst((uint16_t*)base + idx, to_bf16(v)); }
+    __device__ static u32x2 pack4(f32x4 v) { return __builtin_bit_cast(u32x2, __builtin_convertvector(v, bf16x4)); }
+    __device__ static void store4(void* base, size_t idx, f32x4 v) { gst4((uint16_t*)base + idx, pack4(v)); }
     __device__ static float load(const void* base, size_t idx) {
         return __uint_as_float((uint32_t)((const uint16_t*)base)[idx] << 16);
     }
@@ -228,6 +244,8 @@ template <> struct OpTraits<bf16_t> {
 template <> struct OpTraits<f16_t> {
     static constexpr int bytes = 2;
     __device__ static void store(void* base, size_t idx, float v) { gst((uint16_t*)base + idx, to_f16(v)); }
+    __device__ static u32x2 pack4(f32x4 v) { return __builtin_bit_cast(u32x2, __builtin_convertvector(v, f16x4)); }
+    __device__ static void store4(void* base, size_t idx, f32x4 v) { gst4((uint16_t*)base + idx, pack4(v)); }
     __device__ static float load(const void* base, size_t idx) {
         return (float)__builtin_bit_cast(_Float16, ((const uint16_t*)base)[idx]);
     }
@@ -293,6 +311,9 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
 // stages: *_NS; workgroups per CU the registers are sized for: OCC).  The
 // defaults are the fastest measured on MI355X for the settling phases and the
 // GEMM provider; a -D on the compiler line overrides one to measure another.
+#ifndef PCD_ERR_PD
+#define PCD_ERR_PD 3   // error epilogue: blocks whose M operands are in flight
+#endif
 #ifndef PCD_BIG_RB
 #define PCD_BIG_RB 128
 #endif
@@ -369,12 +390,104 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Row-contiguous stores of one 32 x 32 result block held in the transposed
+// layout (lane l: row l % 32, columns 8g + 4(l/32) + k of group g).  Stored as
+// it is held, one wave store would write 32 rows x 16 or 32 bytes (32 partial
+// cache lines, each its own L2 write); the block goes through an LDS region of
+// the wave's own instead (stage_group per group of four columns, then
+// flush_block) and leaves as whole 128-byte (fp32) or 64-byte (16-bit) row
+// segments.  Rows whose bit is clear in rmask and columns at or past n are not
+// written.  LDS accesses of one wave complete in order, so the region needs no
+// barrier between its uses.
+constexpr int kStageRowBytes = 144;                    // 128 bytes of a row + 16 of padding: conflict-free
+constexpr int kStageWaveBytes = 32 * kStageRowBytes;   // one region
+template <int BYTES, typename Pack>
+__device__ __forceinline__ void stage_group(char* st, int g, f32x4 v, Pack pack) {
+    const int lane = threadIdx.x & 63, lr = lane & 31, half = lane >> 5;
+    if constexpr (BYTES == 4) *(f32x4*)(st + lr * kStageRowBytes + (8 * g + 4 * half) * 4) = v;
+    else *(u32x2*)(st + lr * kStageRowBytes + (8 * g + 4 * half) * 2) = pack(v);
+}
+template <int BYTES>
+__device__ __forceinline__ void flush_block(const char* st, void* out, size_t ld, int row0, int col0, uint64_t rmask,
+                                            int n, bool full) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (BYTES == 4) {
+        static_for<0, 4>([&](auto Pc) PCD_INLINE {
+            const int rr = (lane >> 3) + 8 * decltype(Pc)::value, cc = (lane & 7) * 4;
+            const f32x4 w = *(const f32x4*)(st + rr * kStageRowBytes + cc * 4);
+            float* dst = (float*)out + (size_t)(row0 + rr) * ld + col0 + cc;
+            const bool rv = (rmask >> rr) & 1;
+            if (full || (rv && col0 + cc + 3 < n)) {
+                gst4(dst, w);
+            } else if (rv) {
+                static_for<0, 4>([&](auto K) PCD_INLINE {
+                    constexpr int k = decltype(K)::value;
+                    if (col0 + cc + k < n) gst(dst + k, w[k]);
+                });
+            }
+        });
+    } else {
+        static_for<0, 2>([&](auto Pc) PCD_INLINE {
+            const int rr = (lane >> 2) + 16 * decltype(Pc)::value, cc = (lane & 3) * 8;
+            const u32x4 w = *(const u32x4*)(st + rr * kStageRowBytes + cc * 2);
+            uint16_t* dst = (uint16_t*)out + (size_t)(row0 + rr) * ld + col0 + cc;
+            const bool rv = (rmask >> rr) & 1;
+            if (full || (rv && col0 + cc + 7 < n)) {
+                *(__attribute__((address_space(1))) u32x4*)dst = w;
+            } else if (rv) {
+                static_for<0, 8>([&](auto K) PCD_INLINE {
+                    constexpr int k = decltype(K)::value;
+                    if (col0 + cc + k < n) gst(dst + k, (uint16_t)(w[k / 2] >> (16 * (k % 2))));
+                });
+            }
+        });
+    }
+}
+// The loads' counterpart: an fp32 32 x 32 block read as whole 128-byte rows
+// (lane l: row (l/8) + 8p, columns 4(l%8) .. +3 as raw[p]; rows at or past m
+// and groups at or past n read as zero), then turned into the transposed
+// layout through the wave's region (tr[g] = columns 8g + 4(l/32) .. +3 of row
+// l % 32).  Read transposed directly, every four lanes would ask for four
+// rows, four times the requests of whole rows.
+__device__ __forceinline__ void load_block_rows(f32x4 (&raw)[4], const float* src, size_t ld, int row0, int col0,
+                                                int m, int n) {
+    const int lane = threadIdx.x & 63;
+    static_for<0, 4>([&](auto Pc) PCD_INLINE {
+        constexpr int p = decltype(Pc)::value;
+        const int rr = (lane >> 3) + 8 * p, cc = (lane & 7) * 4;
+        raw[p] = (row0 + rr < m && col0 + cc < n) ? gld4(src + (size_t)(row0 + rr) * ld + col0 + cc) : f32x4{};
+    });
+}
+__device__ __forceinline__ void transpose_block(char* st, const f32x4 (&raw)[4], f32x4 (&tr)[4]) {
+    const int lane = threadIdx.x & 63, lr = lane & 31, half = lane >> 5;
+    static_for<0, 4>([&](auto Pc) PCD_INLINE {
+        constexpr int p = decltype(Pc)::value;
+        *(f32x4*)(st + ((lane >> 3) + 8 * p) * kStageRowBytes + (lane & 7) * 16) = raw[p];
+    });
+    static_for<0, 4>([&](auto G) PCD_INLINE {
+        constexpr int g = decltype(G)::value;
+        tr[g] = *(const f32x4*)(st + lr * kStageRowBytes + (8 * g + 4 * half) * 4);
+    });
+}
+
+template <typename OP> struct PackOp {
+    __device__ u32x2 operator()(f32x4 v) const {
+        if constexpr (OpTraits<OP>::bytes == 2) return OpTraits<OP>::pack4(v);
+        else return u32x2{};
+    }
+};
+
 template <typename OP, int BM, int BN, int EPI>
 __global__ void __launch_bounds__((TileCfg<BM, BN>::NT), (TileCfg<BM, BN>::OCC))
 phase_kernel(const ProblemSet set, const PhaseArgs args) {
     constexpr int OPB = OpTraits<OP>::bytes;
     using C = TileCfg<BM, BN, OPB>;
-    __shared__ __attribute__((aligned(16))) char smem[C::NS * C::stage_bytes];
+    // The stage ring; after the main loop the settling epilogues reuse it as
+    // two store-staging regions per wave.
+    // two store-staging regions per wave and the tile's bias.
+    constexpr int STAGE_END = 2 * C::NWAVES * kStageWaveBytes + BN * 4;
+    constexpr int SMEM = C::NS * C::stage_bytes > STAGE_END ? C::NS * C::stage_bytes : STAGE_END;
+    __shared__ __attribute__((aligned(16))) char smem[SMEM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -536,6 +649,12 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
             b[j] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
         }
     };
+    // The settling epilogues take each block transposed (TR): the B-side
+    // fragment goes in as the MFMA's first operand, so a lane holds one row
+    // and runs of four consecutive columns (the result layout at the top of
+    // this file with rows and columns exchanged), which those epilogues read
+    // and write 16 bytes at a time.
+    constexpr bool TR = EPI == EPI_ERROR || EPI == EPI_UPDATE;
     auto mfmas = [&](const u32x4* a, const u32x4* b) PCD_INLINE {
         if constexpr (F32OP) {
             // K component s of every block before component s + 1 of any.
@@ -544,16 +663,18 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                 static_for<0, C::FM>([&](auto I) PCD_INLINE {
                     static_for<0, C::FN>([&](auto J) PCD_INLINE {
                         constexpr int i = decltype(I)::value, j = decltype(J)::value;
-                        accs[k][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[i][s]), __uint_as_float(b[j][s]),
-                                                                            accs[k][i][j], 0, 0, 0);
+                        const float av = __uint_as_float(a[i][s]), bv = __uint_as_float(b[j][s]);
+                        accs[k][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(TR ? bv : av, TR ? av : bv, accs[k][i][j],
+                                                                            0, 0, 0);
                     });
                 });
             });
         } else {
             static_for<0, C::FM>([&](auto I) PCD_INLINE {
                 static_for<0, C::FN>([&](auto J) PCD_INLINE {
-                    mfma_chunk<OP>(accs[0][decltype(I)::value][decltype(J)::value], a[decltype(I)::value],
-                                   b[decltype(J)::value]);
+                    constexpr int i = decltype(I)::value, j = decltype(J)::value;
+                    if constexpr (TR) mfma_chunk<OP>(accs[0][i][j], b[j], a[i]);
+                    else mfma_chunk<OP>(accs[0][i][j], a[i], b[j]);
                 });
             });
         }
@@ -701,21 +822,29 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     }
 
     // ---- epilogue
-    // Row of register r of a block in row-block i: 8*(r/4) + 4*half + r%4.
+    // FFG and plain epilogues (result layout as at the top of this file): row
+    // of register r of a block in row-block i: 8*(r/4) + 4*half + r%4.
     auto row_of = [&](int i, int r) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
     auto col_of = [&](int j) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + lr; };
-    // In the update and plain epilogues a full tile (every row and column
-    // valid, no ragged rows) takes a path with no per-element test: each
-    // element's offset is the block's base plus a per-register row step, and
-    // the per-problem choices (folded update or not, the C term) are made once
-    // per block.  Partial and ragged tiles test every element.  The error
-    // epilogue tests every element on every tile: without the tests' branches
-    // the compiler hoists its loads and addresses until the 256 x 256 tile
-    // spills registers.
+    // In the plain epilogue a full tile (every row and column valid, no ragged
+    // rows) takes a path with no per-element test: each element's offset is the
+    // block's base plus a per-register row step.  Partial tiles test every
+    // element.
     const int ldo = P.ldo;
     auto rstep = [&](int r) PCD_INLINE { return (size_t)(8 * (r >> 2) + (r & 3)) * ldo; };
     auto base_of = [&](int i, int j) PCD_INLINE { return (size_t)row_of(i, 0) * ldo + col_of(j); };
     const bool full = row0 + BM <= P.M && col0 + BN <= P.N && args.row_req == nullptr;
+    // The settling epilogues (TR): lane l holds row l % 32 of each block, and
+    // register 4g + k of block (i, j) is column tcol(j, g) + k.  Every group of
+    // four registers is loaded in one 16-byte access, the row and column tests
+    // are made per lane and group, not per element, and results leave through
+    // the wave's LDS region as whole row segments (store_block).  Columns at or
+    // past N are never written (the padding of the states stays zero).
+    auto trow = [&](int i) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + lr; };
+    auto tcol = [&](int j, int g) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + 8 * g + 4 * half; };
+    char* wstage = smem + 2 * wave_u * kStageWaveBytes;   // X / M_l values
+    char* wstage2 = wstage + kStageWaveBytes;             // D / operand-copy values
+    if constexpr (TR) __syncthreads();   // every wave is done reading the stage ring
     if constexpr (EPI == EPI_ERROR) {
         // On the 256 x 256 tile (the large 16-bit models), one copy of the
         // epilogue per activation, chosen once per tile: the per-element
@@ -727,71 +856,81 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
             // Blocks b = i*FN + j in order; the M_{l-1} operands of the next PD
             // blocks are in flight while a block computes, so the load latency is
             // paid about once per tile instead of once per block.
-            constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
+            constexpr int NB = C::FM * C::FN, PD = NB < PCD_ERR_PD ? NB : PCD_ERR_PD;
             const float P_low = P.prec, inv2p = 0.5f / P.prec;
             const float eta = args.eta, lam = args.act_reg;
             const bool want_energy = args.energy_part != nullptr;
-            float mv[PD][16];
-            float esum[16];
+            // The tile's bias, once into LDS (registers are short on the
+            // 256 x 256 tile); each group reads its four values from there.
+            float* sbias = (float*)(smem + 2 * C::NWAVES * kStageWaveBytes);
+            for (int c = tid * 4; c < BN; c += C::NT * 4)
+                *(f32x4*)(sbias + c) = col0 + c < P.N ? gld4(P.bias + col0 + c) : f32x4{};
+            __syncthreads();
+            f32x4 mraw[PD][4];
             auto load_block = [&](auto Bc) PCD_INLINE {
                 constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
-                const int col = col_of(j);
-                static_for<0, 16>([&](auto R) PCD_INLINE {
-                    constexpr int r = decltype(R)::value;
-                    const int row = row_of(i, r);
-                    mv[b % PD][r] = (col < P.N && row < P.M) ? gld(P.mlow + (size_t)row * ldo + col) : 0.f;
-                });
+                load_block_rows(mraw[b % PD], P.mlow, ldo, row0 + wm * C::WTM + i * 32, col0 + wn * C::WTN + j * 32,
+                                P.M, P.N);
             };
             static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
+            float esum = 0.f;
+            bool rok = false;
+            uint64_t rmask = 0;
             static_for<0, NB>([&](auto Bc) PCD_INLINE {
                 constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
-                if constexpr (j == 0) static_for<0, 16>([&](auto R) PCD_INLINE { esum[decltype(R)::value] = 0.f; });
-                const int col = col_of(j);
-                const bool cok = col < P.N;
-                const float bj = cok ? gld(P.bias + col) : 0.f;
-                static_for<0, 16>([&](auto R) PCD_INLINE {
-                    constexpr int r = decltype(R)::value;
-                    const int row = row_of(i, r);
-                    if (cok && row < P.M && row_active(args, row)) {
-                        const size_t idx = (size_t)row * ldo + col;
-                        const float pre = acc[i][j][r] + bj;
+                const int row = trow(i);
+                if constexpr (j == 0) {
+                    esum = 0.f;
+                    rok = row < P.M && row_active(args, row);
+                    rmask = __ballot(rok);
+                }
+                f32x4 mv[4];
+                transpose_block(wstage, mraw[b % PD], mv);
+                static_for<0, 4>([&](auto G) PCD_INLINE {
+                    constexpr int g = decltype(G)::value;
+                    const int col = tcol(j, g);
+                    const f32x4 bv = *(const f32x4*)(sbias + (col - col0));
+                    f32x4 dv, xv, ev;
+                    static_for<0, 4>([&](auto K) PCD_INLINE {
+                        constexpr int k = decltype(K)::value;
+                        const float pre = acc[i][j][4 * g + k] + bv[k];
                         float y, dy;
                         act_eval(ACT >= 0 ? ACT : args.act, pre, y, dy);
-                        const float m = mv[b % PD][r];
+                        const float m = mv[g][k];
                         const float e = P_low * (m - y);
-                        const float d = dy * e;
-                        OpTraits<OP>::store(P.dout, idx, d);
+                        dv[k] = dy * e;
                         // The state's own part of its update, folded here while
                         // M_{l-1} is in registers: X = M - eta (e + lambda sign M).
                         // The update phase then only adds eta * (W^T D).
-                        if (P.eout) {
-                            float g = e;
-                            if (lam > 0.f) g += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
-                            gst(P.eout + idx, m - eta * g);
-                        }
-                        esum[r] += e * e * inv2p;
+                        float gr = e;
+                        if (lam > 0.f) gr += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
+                        xv[k] = m - eta * gr;
+                        ev[k] = e;
+                    });
+                    float es = 0.f;
+                    if (rok && col + 3 < P.N) {
+                        es = ev[0] * ev[0] + ev[1] * ev[1] + ev[2] * ev[2] + ev[3] * ev[3];
+                    } else if (rok) {
+                        static_for<0, 4>([&](auto K) PCD_INLINE {
+                            constexpr int k = decltype(K)::value;
+                            if (col + k < P.N) es += ev[k] * ev[k];
+                        });
                     }
+                    esum += es * inv2p;
+                    stage_group<4>(wstage, g, xv, PackOp<OP>{});
+                    stage_group<OPB>(wstage2, g, dv, PackOp<OP>{});
                 });
+                const int brow = row0 + wm * C::WTM + i * 32, bcol = col0 + wn * C::WTN + j * 32;
+                if (P.eout) flush_block<4>(wstage, P.eout, ldo, brow, bcol, rmask, P.N, full);
+                flush_block<OPB>(wstage2, P.dout, ldo, brow, bcol, rmask, P.N, full);
                 if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
                 if constexpr (j == C::FN - 1) {
                     if (want_energy) {
-                        static_for<0, 16>([&](auto R) PCD_INLINE {
-                            constexpr int r = decltype(R)::value;
-                            float v = esum[r];
-                            v += __shfl_xor(v, 16);
-                            v += __shfl_xor(v, 8);
-                            v += __shfl_xor(v, 4);
-                            v += __shfl_xor(v, 2);
-                            v += __shfl_xor(v, 1);
-                            esum[r] = v;
-                        });
-                        if (lr == 0) {
+                        // The two half-waves hold the two column halves of each group.
+                        const float v = esum + __shfl_xor(esum, 32);
+                        if (half == 0 && row < P.M) {
                             const int slot = P.slot_base + tn * C::WN + wn;
-                            static_for<0, 16>([&](auto R) PCD_INLINE {
-                                constexpr int r = decltype(R)::value;
-                                const int row = row_of(i, r);
-                                if (row < P.M) gst(args.energy_part + (size_t)slot * args.ldp + row, esum[r]);
-                            });
+                            gst(args.energy_part + (size_t)slot * args.ldp + row, v);
                         }
                     }
                 }
@@ -814,86 +953,52 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
         // lambda sign M_l) having been written by the error phase; the top
         // layer (E = 0) reads M_l itself: M_l -= eta (lambda sign M_l - G).
         // The operand of the next PD blocks is in flight while a block computes.
-        auto epilogue = [&](auto FullC) PCD_INLINE {
-            constexpr bool FULL = decltype(FullC)::value;
-            constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
-            const float eta = args.eta, lam = args.act_reg;
-            const bool folded = P.eself != nullptr;
-            const float* src = folded ? P.eself : P.m;
-            float xv[PD][16];
-            auto load_block = [&](auto Bc) PCD_INLINE {
-                constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
-                if constexpr (FULL) {
-                    static_for<0, 16>([&](auto R) PCD_INLINE {
-                        constexpr int r = decltype(R)::value;
-                        xv[b % PD][r] = gld(src + base_of(i, j) + rstep(r));
-                    });
-                } else {
-                    const int col = col_of(j);
-                    static_for<0, 16>([&](auto R) PCD_INLINE {
-                        constexpr int r = decltype(R)::value;
-                        const int row = row_of(i, r);
-                        xv[b % PD][r] = (col < P.N && row < P.M) ? gld(src + (size_t)row * ldo + col) : 0.f;
-                    });
-                }
-            };
-            static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
-            static_for<0, NB>([&](auto Bc) PCD_INLINE {
-                constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
-                if constexpr (FULL) {
-                    float mn[16];
-                    if (folded) {
-                        static_for<0, 16>([&](auto R) PCD_INLINE {
-                            constexpr int r = decltype(R)::value;
-                            mn[r] = xv[b % PD][r] + eta * acc[i][j][r];
-                        });
-                    } else {
-                        static_for<0, 16>([&](auto R) PCD_INLINE {
-                            constexpr int r = decltype(R)::value;
-                            const float x = xv[b % PD][r];
-                            float grad = -acc[i][j][r];
-                            if (lam > 0.f) grad += lam * (x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f));
-                            mn[r] = x - eta * grad;
-                        });
-                    }
-                    static_for<0, 16>([&](auto R) PCD_INLINE {
-                        constexpr int r = decltype(R)::value;
-                        gst(P.m + base_of(i, j) + rstep(r), mn[r]);
-                    });
-                    if (P.mop)
-                        static_for<0, 16>([&](auto R) PCD_INLINE {
-                            constexpr int r = decltype(R)::value;
-                            OpTraits<OP>::store(P.mop, base_of(i, j) + rstep(r), mn[r]);
-                        });
-                } else {
-                    const int col = col_of(j);
-                    if (col < P.N) {
-                        static_for<0, 16>([&](auto R) PCD_INLINE {
-                            constexpr int r = decltype(R)::value;
-                            const int row = row_of(i, r);
-                            if (row < P.M && row_active(args, row)) {
-                                const size_t idx = (size_t)row * ldo + col;
-                                const float x = xv[b % PD][r];
-                                float m;
-                                if (folded) {
-                                    m = x + eta * acc[i][j][r];
-                                } else {
-                                    float grad = -acc[i][j][r];
-                                    if (lam > 0.f) grad += lam * (x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f));
-                                    m = x - eta * grad;
-                                }
-                                gst(P.m + idx, m);
-                                if (P.mop) OpTraits<OP>::store(P.mop, idx, m);
-                            }
-                        });
-                    }
-                }
-                if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
-                __builtin_amdgcn_sched_barrier(0);
-            });
+        constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
+        const float eta = args.eta, lam = args.act_reg;
+        const bool folded = P.eself != nullptr;
+        const float* src = folded ? P.eself : P.m;
+        f32x4 xraw[PD][4];
+        auto load_block = [&](auto Bc) PCD_INLINE {
+            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+            load_block_rows(xraw[b % PD], src, ldo, row0 + wm * C::WTM + i * 32, col0 + wn * C::WTN + j * 32, P.M,
+                            P.N);
         };
-        if (full) epilogue(std::true_type{});
-        else epilogue(std::false_type{});
+        static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
+        uint64_t rmask = 0;
+        static_for<0, NB>([&](auto Bc) PCD_INLINE {
+            constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
+            if constexpr (j == 0) {
+                const int row = trow(i);
+                rmask = __ballot(row < P.M && row_active(args, row));
+            }
+            f32x4 xv[4];
+            transpose_block(wstage, xraw[b % PD], xv);
+            static_for<0, 4>([&](auto G) PCD_INLINE {
+                constexpr int g = decltype(G)::value;
+                f32x4 mn;
+                if (folded) {
+                    static_for<0, 4>([&](auto K) PCD_INLINE {
+                        constexpr int k = decltype(K)::value;
+                        mn[k] = xv[g][k] + eta * acc[i][j][4 * g + k];
+                    });
+                } else {
+                    static_for<0, 4>([&](auto K) PCD_INLINE {
+                        constexpr int k = decltype(K)::value;
+                        const float x = xv[g][k];
+                        float grad = -acc[i][j][4 * g + k];
+                        if (lam > 0.f) grad += lam * (x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f));
+                        mn[k] = x - eta * grad;
+                    });
+                }
+                stage_group<4>(wstage, g, mn, PackOp<OP>{});
+                if (P.mop) stage_group<OPB>(wstage2, g, mn, PackOp<OP>{});
+            });
+            const int brow = row0 + wm * C::WTM + i * 32, bcol = col0 + wn * C::WTN + j * 32;
+            flush_block<4>(wstage, P.m, ldo, brow, bcol, rmask, P.N, full);
+            if (P.mop) flush_block<OPB>(wstage2, P.mop, ldo, brow, bcol, rmask, P.N, full);
+            if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
+            __builtin_amdgcn_sched_barrier(0);
+        });
     } else if constexpr (EPI == EPI_FFG) {
         static_for<0, C::FM>([&](auto I) PCD_INLINE {
             constexpr int i = decltype(I)::value;

@@ -241,6 +241,7 @@ struct Workspace {
     int* split_count = nullptr;        // split-K finished-range counters, zero between launches
     int* act_tm = nullptr;             // ragged: row tiles still running at the current step [cap / 64]
     int* act_count = nullptr;          // ragged: their number
+    void* rg_tables = nullptr;         // ragged: per-call tables (see pcd_pc_relax_ragged), sized for cap rows
     hipStream_t capture = nullptr;     // private stream used for graph capture
     std::vector<std::unique_ptr<Plan>> plans;
     std::vector<void*> owned;          // every hipMalloc'ed buffer
@@ -249,6 +250,10 @@ struct Workspace {
 struct Plan {
     int batch = 0, steps = 0, want_energy = 0, clamp_top = 0;
     Tile tile{0, 0};
+    // ragged loops (requests > 0): their tables live in the workspace at
+    // offsets fixed by (batch, requests), so these complete the key
+    int requests = 0, exit_rule = 0;
+    float exit_thr = 0.f;
     float* energy_out = nullptr;       // [steps x batch]
     hipGraphExec_t exec = nullptr;
     hipGraph_t graph = nullptr;
@@ -290,6 +295,7 @@ void free_workspace(Workspace& w) {
     w.plans.clear();
     for (void* p : w.owned) (void)hipFree(p);
     w.owned.clear();
+    w.rg_tables = nullptr;
     if (w.capture) (void)hipStreamDestroy(w.capture);
     w.capture = nullptr;
 }
@@ -708,12 +714,16 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
     return PCD_SUCCESS;
 }
 
-Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy, int clamp_top, Tile tile,
-               int* status) {
+// The cached graph of the T-step loop described by r (its energy buffer is the
+// plan's own when want_energy is set), captured on first use.
+Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, int* status) {
     *status = PCD_SUCCESS;
+    const int requests = r.row_req ? r.requests : 0;
     for (auto& p : w->plans)
-        if (p->batch == batch && p->steps == steps && p->want_energy == want_energy && p->clamp_top == clamp_top &&
-            p->tile.m == tile.m && p->tile.n == tile.n) {
+        if (p->batch == r.batch && p->steps == r.steps && p->want_energy == want_energy &&
+            p->clamp_top == r.clamp_top && p->tile.m == r.tile.m && p->tile.n == r.tile.n &&
+            p->requests == requests && (requests == 0 || (p->exit_rule == r.exit_rule &&
+                                                          std::memcmp(&p->exit_thr, &r.exit_thr, 4) == 0))) {
             p->last_use = ++m->clock;
             return p.get();
         }
@@ -726,35 +736,32 @@ Plan* get_plan(pcd_model* m, Workspace* w, int batch, int steps, int want_energy
         w->plans.erase(it);
     }
     std::unique_ptr<Plan> p(new Plan());
-    p->batch = batch;
-    p->steps = steps;
+    p->batch = r.batch;
+    p->steps = r.steps;
     p->want_energy = want_energy;
-    p->clamp_top = clamp_top;
-    p->tile = tile;
+    p->clamp_top = r.clamp_top;
+    p->tile = r.tile;
+    p->requests = requests;
+    p->exit_rule = requests ? r.exit_rule : 0;
+    p->exit_thr = requests ? r.exit_thr : 0.f;
     p->last_use = ++m->clock;
     if (want_energy) {
-        hipError_t e = hipMalloc(&p->energy_out, (size_t)steps * batch * 4);
+        hipError_t e = hipMalloc(&p->energy_out, (size_t)r.steps * r.batch * 4);
         if (e != hipSuccess) { *status = from_hip(e, "hipMalloc(energy)"); return nullptr; }
     }
-    if (m->use_graph) {
-        hipStream_t cs = w->capture;
-        hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
-        if (e != hipSuccess) { *status = from_hip(e, "hipStreamBeginCapture"); return nullptr; }
-        RelaxSpec r;
-        r.batch = batch;
-        r.steps = steps;
-        r.tile = tile;
-        r.clamp_top = clamp_top;
-        r.energy_out = p->energy_out;
-        int st = enqueue_relax(m, w, r, cs, nullptr);
-        hipGraph_t g = nullptr;
-        e = hipStreamEndCapture(cs, &g);
-        if (st) { if (g) (void)hipGraphDestroy(g); *status = st; return nullptr; }
-        if (e != hipSuccess) { *status = from_hip(e, "hipStreamEndCapture"); return nullptr; }
-        p->graph = g;
-        e = hipGraphInstantiate(&p->exec, g, nullptr, nullptr, 0);
-        if (e != hipSuccess) { *status = from_hip(e, "hipGraphInstantiate"); return nullptr; }
-    }
+    hipStream_t cs = w->capture;
+    hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) { *status = from_hip(e, "hipStreamBeginCapture"); return nullptr; }
+    RelaxSpec rc = r;
+    if (want_energy) rc.energy_out = p->energy_out;
+    int st = enqueue_relax(m, w, rc, cs, nullptr);
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(cs, &g);
+    if (st) { if (g) (void)hipGraphDestroy(g); *status = st; return nullptr; }
+    if (e != hipSuccess) { *status = from_hip(e, "hipStreamEndCapture"); return nullptr; }
+    p->graph = g;
+    e = hipGraphInstantiate(&p->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) { *status = from_hip(e, "hipGraphInstantiate"); return nullptr; }
     w->plans.push_back(std::move(p));
     return w->plans.back().get();
 }
@@ -787,7 +794,7 @@ int run_relax(pcd_model* m, Workspace* w, int batch, int steps, int clamp_top, i
         return PCD_SUCCESS;
     }
     int st = PCD_SUCCESS;
-    Plan* p = get_plan(m, w, batch, steps, want_energy, clamp_top, r.tile, &st);
+    Plan* p = get_plan(m, w, r, want_energy, &st);
     if (!p) return st;
     HIP_TRY(hipGraphLaunch(p->exec, s));
     *energy = p->energy_out;
@@ -1349,19 +1356,25 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
     const int L = m->L;
     const Tile tile = choose_tile(m, rows);
     // Small per-call tables: rows' request ids, request offsets, exit state.
-    std::vector<int> row_req(rows);
-    for (int r = 0; r < requests; ++r)
-        for (int i = row_offsets[r]; i < row_offsets[r + 1]; ++i) row_req[i] = r;
+    // They live in a workspace buffer sized for the largest call the
+    // workspace takes (rows <= cap, requests <= rows), at offsets fixed by
+    // (rows, requests), so the cached graph of a loop of the same shape finds
+    // this call's tables where it was captured.
     const size_t tbytes = (size_t)rows * 4 + (size_t)(requests + 1) * 4 + (size_t)requests * 4 * 3;
-    void* tables = nullptr;
-    if (int st = pool_alloc(&tables, tbytes, s)) return st;
+    if (!w->rg_tables) {
+        const size_t cap_bytes = (size_t)w->cap * 4 + (size_t)(w->cap + 1) * 4 + (size_t)w->cap * 4 * 3;
+        if (int st = dev_alloc_zero(w->owned, &w->rg_tables, cap_bytes)) return st;
+    }
+    void* tables = w->rg_tables;
     int* d_row_req = (int*)tables;
     int* d_offsets = d_row_req + rows;
     int* d_done = d_offsets + requests + 1;
     float* d_prev = (float*)(d_done + requests);
     float* d_last = d_prev + requests;
     std::vector<char> host(tbytes, 0);
-    std::memcpy(host.data(), row_req.data(), (size_t)rows * 4);
+    int* h_row_req = (int*)host.data();
+    for (int r = 0; r < requests; ++r)
+        for (int i = row_offsets[r]; i < row_offsets[r + 1]; ++i) h_row_req[i] = r;
     std::memcpy(host.data() + (size_t)rows * 4, row_offsets, (size_t)(requests + 1) * 4);
     std::memcpy(host.data() + (size_t)(rows + requests + 1) * 4, steps, (size_t)requests * 4);
     int st = PCD_SUCCESS;
@@ -1371,9 +1384,6 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
                              hipMemcpyDeviceToDevice, s);
     if (e != hipSuccess) st = from_hip(e, "ragged upload");
     if (!st) {
-        // With the profile option, every phase launch is timed (the ragged
-        // loop always runs eagerly).
-        PhaseTimer timer;
         RelaxSpec r;
         r.batch = rows;
         r.steps = tmax;
@@ -1386,10 +1396,23 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
         r.exit_thr = exit_threshold;
         r.prev_energy = d_prev;
         r.last_energy = d_last;
-        st = enqueue_relax(m, w, r, s, m->profile ? &timer : nullptr);
-        if (m->profile) {
-            int st2 = collect_timer(m, timer, s);
-            if (!st) st = st2;
+        if (m->profile || !m->use_graph) {
+            // With the profile option, every phase launch is timed (eagerly).
+            PhaseTimer timer;
+            st = enqueue_relax(m, w, r, s, m->profile ? &timer : nullptr);
+            if (m->profile) {
+                int st2 = collect_timer(m, timer, s);
+                if (!st) st = st2;
+            }
+        } else {
+            // The loop of tmax steps as one graph: requests that have exited
+            // keep their states, and steps after every request has exited
+            // find no running row tile and return at once.
+            Plan* p = get_plan(m, w, r, 0, &st);
+            if (p) {
+                e = hipGraphLaunch(p->exec, s);
+                if (e != hipSuccess) st = from_hip(e, "hipGraphLaunch");
+            }
         }
     }
     if (!st) st = copy_out_rows(out_top, m->s[L - 1], w->M[L - 1], m->P[L - 1], rows, s);
@@ -1401,7 +1424,7 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
         if (e != hipSuccess) st = from_hip(e, "ragged download");
     }
     if (!st && out_energy) std::memcpy(out_energy, last.data(), (size_t)requests * 4);
-    pool_free(tables, s);
+    if (st) (void)hipStreamSynchronize(s);   // the upload reads `host` until the stream reaches it
     return st;
 }
 

@@ -228,6 +228,43 @@ def test_ragged_requests_with_exit(oracle):
         m.close()
 
 
+def test_ragged_graph_matches_eager_and_takes_new_tables(oracle):
+    # The ragged loop replays a cached graph for calls of one shape (rows,
+    # requests, longest budget, exit rule and threshold); each call's own
+    # request budgets and inputs reach it through the workspace tables.
+    from predicitivecoding_amd import PcDeviceModel
+    sizes = [40, 64, 32, 8]
+    snap, W, b, P, _ = build_case(sizes, "tanh", 0.1, seed=21)
+    rng = np.random.default_rng(5)
+    counts = [3, 40, 1, 12, 7]
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    rows = int(offs[-1])
+    calls = []
+    for _ in range(3):
+        x = (rng.standard_normal((rows, sizes[0])) * 0.3).astype(np.float32)
+        steps = rng.integers(2, 30, len(counts)).astype(np.int32)
+        steps[0] = 30   # the same longest budget: every call hits the same cached graph
+        calls.append((x, steps))
+    out = {}
+    for graph in (1, 0):
+        m = PcDeviceModel(snap, "f32")
+        try:
+            m.set_option("use_graph", graph)
+            out[graph] = [m.relax_ragged(x, offs, steps, rule, thr)
+                          for x, steps in calls for rule, thr in [("none", 0.0), ("absolute", 0.8)]]
+        finally:
+            m.close()
+    for g, e in zip(out[1], out[0]):
+        for a, c in zip(g, e):
+            assert np.array_equal(a, c)
+    for (x, steps), k in zip(calls, range(0, 6, 2)):
+        used, fe, top = out[1][k + 1]
+        rused, rfe, rtop = oracle.ragged_relax(sizes, "tanh", 0.1, W, b, P, x, offs, steps, "absolute", 0.8)
+        assert np.array_equal(used, rused)
+        assert max_rel(top, rtop) < 1e-4 and max_rel(fe, rfe) < 1e-4
+        assert np.array_equal(out[1][k][0], steps)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("tile", [64, 128, 256])
 def test_ragged_tile_list_matches_full_grid(oracle, dtype, tile):
