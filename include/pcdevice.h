@@ -278,7 +278,9 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
 
 /* Relaxation options (no counterpart in the reference; tuning and profiling
  * hooks for the host wrappers and the benchmark):
- *   use_graph    capture the T-step loop in a hipGraph (default 1)
+ *   use_graph    capture the T-step loop in a hipGraph and replay it (default
+ *                1); graphs are cached per call shape (batch, steps, tile, and
+ *                for pcd_pc_relax_ragged also requests, exit rule, threshold)
  *   tile, tile_n force a GEMM tile (0 = automatic choice): tile sets rows and
  *                columns, tile_n then the columns; supported 64 x 64,
  *                64 x 128, 64 x 256, 128 x 128, 256 x 128, 256 x 256
