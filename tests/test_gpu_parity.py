@@ -228,6 +228,46 @@ def test_ragged_requests_with_exit(oracle):
         m.close()
 
 
+def test_two_threads_on_two_streams_share_one_model():
+    # The library's threading contract: one model serves several streams at
+    # once, each (model, stream) pair with its own workspace and cached
+    # graphs.  Two host threads settle their own batches on their own streams
+    # (ctypes releases the GIL, so the calls overlap); every result equals the
+    # single-threaded one bit for bit.
+    import threading
+    from predicitivecoding_amd import PcDeviceModel, Stream
+    snap, W, b, P, x = build_case([96, 128, 64, 16], "tanh", 0.1, batch=200, seed=29)
+    xs = [x, x[:77]]
+    m = PcDeviceModel(snap, "f32")
+    streams = [Stream(), Stream()]
+    try:
+        ref = [m.relax(xi, 9, want_energy=True) for xi in xs]
+        results = [[None] * 6 for _ in xs]
+        errors = []
+
+        def work(k):
+            try:
+                for rep in range(6):
+                    results[k][rep] = m.relax(xs[k], 9, want_energy=True, stream=streams[k])
+            except Exception as e:  # reported below, on the test's thread
+                errors.append(e)
+
+        threads = [threading.Thread(target=work, args=(k,)) for k in range(len(xs))]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=100)
+        assert not any(t.is_alive() for t in threads), "a settling thread did not finish"
+        assert not errors, errors
+        for k in range(len(xs)):
+            for top, _, en in results[k]:
+                assert np.array_equal(top, ref[k][0]) and np.array_equal(en, ref[k][2])
+    finally:
+        for st in streams:
+            st.close()
+        m.close()
+
+
 def test_ragged_graph_matches_eager_and_takes_new_tables(oracle):
     # The ragged loop replays a cached graph for calls of one shape (rows,
     # requests, longest budget, exit rule and threshold); each call's own
