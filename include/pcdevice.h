@@ -291,10 +291,12 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *   k_stagger    S > 1: GEMM tile (tm, tn) of a settling phase sums its K
  *                stages starting at stage (tm + tn) % S, so tiles sharing
  *                operand rows do not all miss in L2 on the same rows at once;
- *                0 or 1: every tile sums from stage 0.  Default 16 for 16-bit
- *                models, 0 for fp32.  With S > 1 a row's bits depend on where
- *                it falls in the batch (they stay the same run to run); with
- *                0 a row's result is independent of the other rows.  At most 64.
+ *                0 or 1: every tile sums from stage 0; -1: automatic, a
+ *                quarter of the longest K sweep's stages (at least 2).  Default
+ *                -1 for 16-bit models, 0 for fp32.  With S > 1 a row's bits
+ *                depend on where it falls in the batch (they stay the same run
+ *                to run); with 0 a row's result is independent of the other
+ *                rows.  At most 64.
  *   ragged_tiles 1: before each step of pcd_pc_relax_ragged, list the row tiles
  *                that still hold a running row, and deal only those tiles over
  *                the XCDs (default); 0: launch every tile, and let tiles whose

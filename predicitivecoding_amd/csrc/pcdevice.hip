@@ -222,7 +222,11 @@ constexpr int kRowPad = 256;    // row dims padded to the widest tile
 // and 12 x 8192 bf16 networks: 7-10% faster than no stagger, and better than 4
 // or 8 offsets).  fp32 gained nothing measurable and keeps it off, which also
 // keeps every row's result independent of the other rows in the batch.
-constexpr int kKStagger16 = 16;
+// K stagger of a 16-bit GEMM sweeping nk stages when the option is left
+// automatic: a quarter of the stages (measured best at nk = 64 and 128: c3's
+// and c5's settling phases, the 8192^3 provider GEMM), within [2, kMaxKStagger].
+constexpr int kKStaggerAuto = -1;
+int auto_k_stagger(int nk);
 constexpr int kMaxKStagger = 64;
 
 struct Plan;
@@ -277,7 +281,7 @@ struct pcd_model {
     std::vector<std::unique_ptr<Workspace>> ws;
     // options
     int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED, split_k = 1;
-    int k_stagger = 0;                  // settling phases only (kKStagger16 for 16-bit operands)
+    int k_stagger = 0;                  // settling phases: kKStaggerAuto (16-bit default), 0 off, or a fixed value
     int ragged_tiles = 1;               // ragged phases deal only the row tiles still running
     float prof_err_ms = 0.f, prof_upd_ms = 0.f;
     int prof_launches = 0;
@@ -553,6 +557,8 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
     *nslots = slot;
 }
 
+int auto_k_stagger(int nk) { return std::max(2, std::min(kMaxKStagger, nk / 4)); }
+
 PhaseArgs base_args(const pcd_model* m, const Workspace* w, int batch, int nslots) {
     PhaseArgs a;
     std::memset(&a, 0, sizeof a);
@@ -630,6 +636,12 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
     int nslots = 0;
     build_phase_sets(m, w, batch, tile, r.clamp_top, err, upd, &nslots);
     PhaseArgs args = base_args(m, w, batch, nslots);
+    if (args.k_stagger == kKStaggerAuto) {
+        // the settling phases' longest K sweep at this tile (padded sizes are
+        // both phases' K)
+        const int maxp = *std::max_element(m->P.begin(), m->P.end());
+        args.k_stagger = auto_k_stagger(maxp / stage_k(m->dtype, tile));
+    }
     args.row_req = r.row_req;
     args.done_at = r.done_at;
     const bool need_energy = r.energy_out != nullptr || r.row_req != nullptr;
@@ -1090,7 +1102,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     std::memset(&a, 0, sizeof a);
     a.alpha = 1.f;
     a.beta = beta;
-    a.k_stagger = dtype == PCD_F32 ? 0 : kKStagger16;   // 8192^3 bf16: +2.6%
+    a.k_stagger = dtype == PCD_F32 ? 0 : auto_k_stagger(kp / stage_k(dtype, tile));
     if (!st) st = launch_phase(dtype, tile, EPI_PLAIN, sets[0], a, s);
     release();
     if (part) {
@@ -1150,7 +1162,7 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
     m->act = activation;
     m->ffg = ffg ? 1 : 0;
     m->dtype = dtype;
-    m->k_stagger = dtype == PCD_F32 ? 0 : kKStagger16;
+    m->k_stagger = dtype == PCD_F32 ? 0 : kKStaggerAuto;
     m->eta = eta;
     m->act_reg = act_reg;
     m->prec.assign(precisions, precisions + levels);
@@ -1267,8 +1279,8 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
         m->tile_order = value;
     } else if (n == "ragged_tiles") m->ragged_tiles = value ? 1 : 0;
     else if (n == "k_stagger") {
-        if (value < 0 || value > kMaxKStagger)
-            return fail(PCD_INVALID_VALUE, "k_stagger must be 0 (off) to %d", kMaxKStagger);
+        if (value < kKStaggerAuto || value > kMaxKStagger)
+            return fail(PCD_INVALID_VALUE, "k_stagger must be -1 (automatic), 0 (off) or up to %d", kMaxKStagger);
         m->k_stagger = value;
     } else return fail(PCD_INVALID_VALUE, "unknown option '%s'", name);
     // cached graphs were captured with the old options

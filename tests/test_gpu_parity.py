@@ -90,16 +90,21 @@ def test_k_stagger_parity(oracle, dtype, stagger, tile):
 
 def test_k_stagger_changes_only_the_summation_order():
     # the option is really applied (fp32 sums in another order differ in the
-    # last bits) and the default of a 16-bit model is on: setting the default
-    # value explicitly changes nothing
+    # last bits) and the default of a 16-bit model is the automatic stride, a
+    # quarter of the longest K sweep's stages: here K pads to 576, 9 stages of
+    # 64 bf16 on the 64 x 64 tile, so 2.  Setting that value, or -1, explicitly
+    # changes nothing.
     snap, _, _, _, x = build_case([300, 520, 260], "tanh", 0.1, batch=600, seed=20)
     a, _, ea = run_gpu(snap, x, 5, energy=True, options={"tile": 64})
     c, _, ec = run_gpu(snap, x, 5, energy=True, options={"tile": 64, "k_stagger": 16})
     assert not np.array_equal(ea, ec)
     assert max_rel(c, a) < 1e-5 and max_rel(ec, ea) < 1e-5
     d, _, ed = run_gpu(snap, x, 5, dtype="bf16", energy=True, options={"tile": 64})
-    e, _, ee = run_gpu(snap, x, 5, dtype="bf16", energy=True, options={"tile": 64, "k_stagger": 16})
-    assert np.array_equal(d, e) and np.array_equal(ed, ee)
+    for explicit in (2, -1):
+        e, _, ee = run_gpu(snap, x, 5, dtype="bf16", energy=True, options={"tile": 64, "k_stagger": explicit})
+        assert np.array_equal(d, e) and np.array_equal(ed, ee), explicit
+    f, _, ef = run_gpu(snap, x, 5, dtype="bf16", energy=True, options={"tile": 64, "k_stagger": 0})
+    assert not np.array_equal(ed, ef)
 
 
 def test_k_stagger_off_keeps_16bit_rows_independent():
@@ -116,10 +121,10 @@ def test_k_stagger_option_values():
     snap, _, _, _, _ = build_case([16, 8], "tanh", 0.1, batch=2)
     m = PcDeviceModel(snap, "bf16")
     try:
-        for bad in (-1, 65):
+        for bad in (-2, 65):
             with pytest.raises(DeviceException):
                 m.set_option("k_stagger", bad)
-        for ok in (0, 1, 2, 64):
+        for ok in (0, 1, 2, 64, -1):   # -1: back to the automatic stride
             m.set_option("k_stagger", ok)
     finally:
         m.close()
