@@ -292,7 +292,8 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *                stages starting at stage (tm + tn) % S, so tiles sharing
  *                operand rows do not all miss in L2 on the same rows at once;
  *                0 or 1: every tile sums from stage 0; -1: automatic, a
- *                quarter of the longest K sweep's stages (at least 2).  Default
+ *                quarter of the longest K sweep's stages, half of them when
+ *                the batch fits one row tile (at least 2).  Default
  *                -1 for 16-bit models, 0 for fp32.  With S > 1 a row's bits
  *                depend on where it falls in the batch (they stay the same run
  *                to run); with 0 a row's result is independent of the other

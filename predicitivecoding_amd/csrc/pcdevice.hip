@@ -224,9 +224,12 @@ constexpr int kRowPad = 256;    // row dims padded to the widest tile
 // keeps every row's result independent of the other rows in the batch.
 // K stagger of a 16-bit GEMM sweeping nk stages when the option is left
 // automatic: a quarter of the stages (measured best at nk = 64 and 128: c3's
-// and c5's settling phases, the 8192^3 provider GEMM), within [2, kMaxKStagger].
+// and c5's settling phases, the 8192^3 provider GEMM); half of them when the
+// rows fit one row tile, where no two tiles share weight rows and the stride
+// only spreads the weight streams (c5's network at 64 rows), within
+// [2, kMaxKStagger].
 constexpr int kKStaggerAuto = -1;
-int auto_k_stagger(int nk);
+int auto_k_stagger(int nk, bool one_row_tile = false);
 constexpr int kMaxKStagger = 64;
 
 struct Plan;
@@ -557,7 +560,9 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
     *nslots = slot;
 }
 
-int auto_k_stagger(int nk) { return std::max(2, std::min(kMaxKStagger, nk / 4)); }
+int auto_k_stagger(int nk, bool one_row_tile) {
+    return std::max(2, std::min(kMaxKStagger, nk / (one_row_tile ? 2 : 4)));
+}
 
 PhaseArgs base_args(const pcd_model* m, const Workspace* w, int batch, int nslots) {
     PhaseArgs a;
@@ -640,7 +645,7 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
         // the settling phases' longest K sweep at this tile (padded sizes are
         // both phases' K)
         const int maxp = *std::max_element(m->P.begin(), m->P.end());
-        args.k_stagger = auto_k_stagger(maxp / stage_k(m->dtype, tile));
+        args.k_stagger = auto_k_stagger(maxp / stage_k(m->dtype, tile), batch <= tile.m);
     }
     args.row_req = r.row_req;
     args.done_at = r.done_at;
