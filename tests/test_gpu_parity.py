@@ -150,6 +150,30 @@ def test_repeated_calls_and_changing_batches(oracle):
         m.close()
 
 
+def test_graph_cache_eviction_and_recapture():
+    # At most 8 cached graphs per (model, stream): ten call shapes, twice
+    # over, evict and capture again; every replay equals the eager result.
+    snap, W, b, P, x = build_case([48, 96, 24], "tanh", 0.1, batch=90, seed=31)
+    shapes = [(90, 3), (1, 4), (17, 5), (64, 3), (65, 6), (33, 2), (90, 7), (2, 9), (50, 5), (80, 4)]
+    from predicitivecoding_amd import PcDeviceModel
+    eager = {}
+    m = PcDeviceModel(snap, "f32")
+    try:
+        m.set_option("use_graph", 0)
+        for B, T in shapes:
+            eager[B, T] = m.relax(x[:B], T, want_energy=True)
+    finally:
+        m.close()
+    m = PcDeviceModel(snap, "f32")
+    try:
+        for _ in range(2):
+            for B, T in shapes:
+                top, _, en = m.relax(x[:B], T, want_energy=True)
+                assert np.array_equal(top, eager[B, T][0]) and np.array_equal(en, eager[B, T][2]), (B, T)
+    finally:
+        m.close()
+
+
 def test_rows_are_independent_bit_for_bit():
     snap, W, b, P, x = build_case([80, 64, 40], "tanh", 0.1, batch=200, seed=13)
     perm = np.random.default_rng(0).permutation(200)
