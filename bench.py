@@ -131,9 +131,25 @@ def make_inputs(cfg, seed=1):
     return torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
 
 
+CPU_REPS = 3
+
+
+def median_run(run, reps=CPU_REPS):
+    """Times `run` (after the caller's warm-up call) `reps` times; returns
+    (median seconds, the run's result), as the reference's bench harness
+    reports MedianMs(reps: 3, warmup: 1) (tools/MixedPrecisionBench/Program.cs:96-101)."""
+    times, out = [], None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        out = run()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), out
+
+
 def cpu_baseline(cfg, W, b, x_host, budget_s=10.0):
     """The oracle's restatement of BatchedPcForward + CpuGemmProvider on the
-    host cores, on a bounded sample: `rows` samples for `steps` steps."""
+    host cores, on a bounded sample: `rows` samples for `steps` steps, the
+    median of three runs."""
     from oracle import pc_oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
     pc_oracle.set_threads(threads)
@@ -147,18 +163,18 @@ def cpu_baseline(cfg, W, b, x_host, budget_s=10.0):
     t0 = time.perf_counter()
     pc_oracle.batched_relax(sizes, act, cfg["eta"], W, b, P, x_host[:rows], 2)
     per = (time.perf_counter() - t0) / (2 * rows)
-    steps = int(max(1, min(cfg["T"], budget_s / max(per * rows, 1e-9))))
+    run_s = budget_s / CPU_REPS
+    steps = int(max(1, min(cfg["T"], run_s / max(per * rows, 1e-9))))
     if steps == cfg["T"]:
-        rows = int(max(rows, min(cfg["batch"], budget_s / max(per * cfg["T"], 1e-9))))
+        rows = int(max(rows, min(cfg["batch"], run_s / max(per * cfg["T"], 1e-9))))
         rows = min(rows, cfg["batch"])
     print(f"# cpu baseline sample: {rows} rows x {steps} steps (calibrated {per * 1e3:.3f} ms per "
-          f"sample-step)", file=sys.stderr, flush=True)
-    t0 = time.perf_counter()
-    pc_oracle.batched_relax(sizes, act, cfg["eta"], W, b, P, x_host[:rows], steps)
-    dt = time.perf_counter() - t0
+          f"sample-step), median of {CPU_REPS}", file=sys.stderr, flush=True)
+    dt, _ = median_run(lambda: pc_oracle.batched_relax(sizes, act, cfg["eta"], W, b, P, x_host[:rows], steps))
     return {"value": rows * steps / dt, "unit": "sample-steps/s", "cores": threads, "kind": "port",
             "sample": f"oracle batched fp32 relaxation (i-k-j row-parallel GEMM as Gemm.cs:106-124), "
-                      f"{rows} of {cfg['batch']} samples x {steps} of {cfg['T']} steps, {dt:.1f} s"}
+                      f"{rows} of {cfg['batch']} samples x {steps} of {cfg['T']} steps, median of {CPU_REPS} "
+                      f"runs of {dt:.1f} s"}
 
 
 def traffic_from_profiles(workload, kernel):
@@ -431,20 +447,30 @@ def cpu_baseline_clamped(cfg, W, b, x_host, labels_host, budget_s=10.0):
     P = [1.0] * len(sizes)
     C = sizes[-1]
     per_sample_rows = C if cfg["mode"] == "classify" else 1
-    done, t0 = 0, time.perf_counter()
-    Wc, bc = W, b
-    while done < cfg["batch"] and (time.perf_counter() - t0) < budget_s:
-        if cfg["mode"] == "classify":
-            pc_oracle.classify(sizes, act, cfg["eta"], W, b, P, x_host[done:done + 1], T)
-        else:
-            Wc, bc, _ = pc_oracle.learn(sizes, act, cfg["eta"], Wc, bc, P, x_host[done:done + 1],
-                                        labels_host[done:done + 1], T, cfg["eta_w"])
-        done += 1
-    dt = time.perf_counter() - t0
+
+    def one_pass():
+        # samples one at a time until a third of the budget is spent; returns
+        # the samples done and the seconds taken
+        done, t0 = 0, time.perf_counter()
+        Wc, bc = W, b
+        while done < cfg["batch"] and (time.perf_counter() - t0) < budget_s / CPU_REPS:
+            if cfg["mode"] == "classify":
+                pc_oracle.classify(sizes, act, cfg["eta"], W, b, P, x_host[done:done + 1], T)
+            else:
+                Wc, bc, _ = pc_oracle.learn(sizes, act, cfg["eta"], Wc, bc, P, x_host[done:done + 1],
+                                            labels_host[done:done + 1], T, cfg["eta_w"])
+            done += 1
+        return done, time.perf_counter() - t0
+
+    one_pass()   # warm-up
+    passes = [one_pass() for _ in range(CPU_REPS)]
+    rates = sorted(d * per_sample_rows * T / t for d, t in passes)
+    done, dt = passes[0]
     name = "Network.PredictCore" if cfg["mode"] == "classify" else "Network.Learn"
-    return {"value": done * per_sample_rows * T / dt, "unit": "sample-steps/s", "cores": 1, "kind": "port",
-            "sample": f"oracle {name} one sample at a time (batch-1 settlings), {done} of {cfg['batch']} samples "
-                      f"x {per_sample_rows} settlings x {T} steps, {dt:.1f} s"}
+    return {"value": rates[len(rates) // 2], "unit": "sample-steps/s", "cores": 1, "kind": "port",
+            "sample": f"oracle {name} one sample at a time (batch-1 settlings), median of {CPU_REPS} passes of "
+                      f"about {done} of {cfg['batch']} samples x {per_sample_rows} settlings x {T} steps "
+                      f"({dt:.1f} s each)"}
 
 
 def bench_gemm(args, cfg):
@@ -495,13 +521,12 @@ def bench_gemm(args, cfg):
         t0 = time.perf_counter()
         pc_oracle.gemm(A[:16].float().cpu().numpy(), bt, "bf16")     # calibration
         per_row = (time.perf_counter() - t0) / 16
-        rows = int(min(m, max(16, args.cpu_budget / 2 / max(per_row, 1e-9))))
+        rows = int(min(m, max(16, args.cpu_budget / 2 / CPU_REPS / max(per_row, 1e-9))))
         a = A[:rows].float().cpu().numpy()
-        t0 = time.perf_counter()
-        pc_oracle.gemm(a, bt, "bf16")
-        dt = time.perf_counter() - t0
+        dt, _ = median_run(lambda: pc_oracle.gemm(a, bt, "bf16"))
         cpu = {"value": 2.0 * rows * n * k / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-               "sample": f"oracle mixed GEMM (Gemm.cs:44-60, i-k-j row-parallel), {rows} of {m} rows, {dt:.1f} s"}
+               "sample": f"oracle mixed GEMM (Gemm.cs:44-60, i-k-j row-parallel), {rows} of {m} rows, median of "
+                         f"{CPU_REPS} runs of {dt:.1f} s"}
         print(f"# cpu baseline: {cpu['value'] * 1e3:.2f} GFLOP/s on {threads} threads", file=sys.stderr, flush=True)
     rec = {
         "metric": "provider GEMM throughput at 1 GPU and % of MFMA roofline", "value": value, "unit": "TFLOP/s",
@@ -532,19 +557,19 @@ def cpu_baseline_ragged(cfg, W, b, x_host, offsets, steps, budget_s=10.0):
     per = (time.perf_counter() - t0) / (2 * n)
     rows = np.diff(offsets)
     k, est = 0, 0.0
-    while k < len(steps) and est + rows[k] * steps[k] * per <= budget_s:
+    while k < len(steps) and est + rows[k] * steps[k] * per <= budget_s / CPU_REPS:
         est += rows[k] * steps[k] * per
         k += 1
     k = max(k, 1)
     sub_off = offsets[:k + 1]
-    t0 = time.perf_counter()
-    used, _, _ = pc_oracle.ragged_relax(sizes, "tanh", cfg["eta"], W, b, P, x_host[:int(sub_off[-1])], sub_off,
-                                        steps[:k], cfg["exit_rule"], cfg["exit_thr"])
-    dt = time.perf_counter() - t0
+    dt, (used, _, _) = median_run(lambda: pc_oracle.ragged_relax(sizes, "tanh", cfg["eta"], W, b, P,
+                                                                 x_host[:int(sub_off[-1])], sub_off, steps[:k],
+                                                                 cfg["exit_rule"], cfg["exit_thr"]))
     done = int(np.sum(rows[:k].astype(np.int64) * used))
     return {"value": done / dt, "unit": "sample-steps/s", "cores": threads, "kind": "port",
             "sample": f"oracle per-request fp32 relaxation with the same exit rule, first {k} of {len(steps)} "
-                      f"requests ({int(sub_off[-1])} rows, {done} sample-steps), {dt:.1f} s"}
+                      f"requests ({int(sub_off[-1])} rows, {done} sample-steps), median of {CPU_REPS} runs of "
+                      f"{dt:.1f} s"}
 
 
 
