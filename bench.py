@@ -597,8 +597,9 @@ def main():
         traffic_from_pmc(args.config, *args.traffic_from, args.traffic_command)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build runs the relaxation on a single MI355X "
-              "(the batch shards over GPUs with no per-step communication; see DESIGN.md).", file=sys.stderr)
+        print("bench.py measures one GPU only: this build runs the relaxation on a single MI355X. The batch "
+              "would shard over GPUs by rows with replicated weights and no per-step communication.",
+              file=sys.stderr)
         sys.exit(2)
 
     if args.calibrate_copy:
