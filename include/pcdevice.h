@@ -302,6 +302,10 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *                that still hold a running row, and deal only those tiles over
  *                the XCDs (default); 0: launch every tile, and let tiles whose
  *                rows have all finished return at once.  Results are the same.
+ *   ragged_order 1: pcd_pc_relax_ragged settles the requests in decreasing
+ *                step budget (rows permuted on the device and back), so rows
+ *                that stop early fill whole row tiles that drop out (default);
+ *                0: in the caller's order.  fp32 results are the same.
  *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
  *                time every phase launch with HIP events (pcd_pc_profile_result) */
 int pcd_pc_set_option(pcd_model* model, const char* name, int value);

@@ -218,4 +218,18 @@ __global__ void bias_update_kernel(const void* __restrict__ d, int ld, int rows,
     }
 }
 
+// Rows of a ragged call between the caller's packing and the settling order:
+// gather dst[i] = src[perm[i]], scatter dst[perm[i]] = src[i], `cols` floats
+// per row.  perm is a permutation of [0, rows).
+__global__ void permute_rows_kernel(const float* __restrict__ src, int lds, float* __restrict__ dst, int ldd,
+                                    const int* __restrict__ perm, int rows, int cols, int gather) {
+    const size_t n = (size_t)rows * cols;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
+        const int i = (int)(e / cols), c = (int)(e % cols);
+        const int p = perm[i];
+        if (gather) dst[(size_t)i * ldd + c] = src[(size_t)p * lds + c];
+        else dst[(size_t)p * ldd + c] = src[(size_t)i * lds + c];
+    }
+}
+
 }  // namespace pcd

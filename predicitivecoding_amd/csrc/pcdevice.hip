@@ -286,6 +286,7 @@ struct pcd_model {
     int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED, split_k = 1;
     int k_stagger = 0;                  // settling phases: kKStaggerAuto (16-bit default), 0 off, or a fixed value
     int ragged_tiles = 1;               // ragged phases deal only the row tiles still running
+    int ragged_order = 1;               // ragged requests settle in decreasing step budget (0: caller's order)
     float prof_err_ms = 0.f, prof_upd_ms = 0.f;
     int prof_launches = 0;
     uint64_t clock = 0;
@@ -1283,6 +1284,7 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
             return fail(PCD_INVALID_VALUE, "tile_order must be 0 (interleaved) or 1 (contiguous)");
         m->tile_order = value;
     } else if (n == "ragged_tiles") m->ragged_tiles = value ? 1 : 0;
+    else if (n == "ragged_order") m->ragged_order = value ? 1 : 0;
     else if (n == "k_stagger") {
         if (value < kKStaggerAuto || value > kMaxKStagger)
             return fail(PCD_INVALID_VALUE, "k_stagger must be -1 (automatic), 0 (off) or up to %d", kMaxKStagger);
@@ -1372,14 +1374,28 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
     if (int st = ensure_workspace(m, s, rows, &w)) return st;
     const int L = m->L;
     const Tile tile = choose_tile(m, rows);
-    // Small per-call tables: rows' request ids, request offsets, exit state.
-    // They live in a workspace buffer sized for the largest call the
-    // workspace takes (rows <= cap, requests <= rows), at offsets fixed by
+    // Settling order: requests by decreasing step budget (stable).  As
+    // requests reach their budgets the rows still running shrink towards a
+    // prefix of the packing, and the row tiles past it drop out of the phases
+    // whole (the per-step tile list deals only running tiles) instead of
+    // staying partly busy.  Option ragged_order = 0 keeps the caller's order.
+    // Rows never interact, so fp32 results do not depend on the order.
+    std::vector<int> order(requests);
+    for (int r = 0; r < requests; ++r) order[r] = r;
+    if (m->ragged_order)
+        std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return steps[a] > steps[b]; });
+    bool identity = true;
+    for (int r = 0; r < requests; ++r) identity = identity && order[r] == r;
+    // Small per-call tables: rows' request ids, request offsets, step
+    // budgets, exit state and (settling order) the caller's row of each
+    // settled row.  They live in a workspace buffer sized for the largest call
+    // the workspace takes (rows <= cap, requests <= rows), at offsets fixed by
     // (rows, requests), so the cached graph of a loop of the same shape finds
     // this call's tables where it was captured.
-    const size_t tbytes = (size_t)rows * 4 + (size_t)(requests + 1) * 4 + (size_t)requests * 4 * 3;
+    const size_t tbytes = (size_t)rows * 4 + (size_t)(requests + 1) * 4 + (size_t)requests * 4 * 3 + (size_t)rows * 4;
     if (!w->rg_tables) {
-        const size_t cap_bytes = (size_t)w->cap * 4 + (size_t)(w->cap + 1) * 4 + (size_t)w->cap * 4 * 3;
+        const size_t cap_bytes = (size_t)w->cap * 4 + (size_t)(w->cap + 1) * 4 + (size_t)w->cap * 4 * 3 +
+                                 (size_t)w->cap * 4;
         if (int st = dev_alloc_zero(w->owned, &w->rg_tables, cap_bytes)) return st;
     }
     void* tables = w->rg_tables;
@@ -1388,17 +1404,35 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
     int* d_done = d_offsets + requests + 1;
     float* d_prev = (float*)(d_done + requests);
     float* d_last = d_prev + requests;
+    int* d_perm = (int*)(d_last + requests);
     std::vector<char> host(tbytes, 0);
     int* h_row_req = (int*)host.data();
-    for (int r = 0; r < requests; ++r)
-        for (int i = row_offsets[r]; i < row_offsets[r + 1]; ++i) h_row_req[i] = r;
-    std::memcpy(host.data() + (size_t)rows * 4, row_offsets, (size_t)(requests + 1) * 4);
-    std::memcpy(host.data() + (size_t)(rows + requests + 1) * 4, steps, (size_t)requests * 4);
+    int* h_offsets = h_row_req + rows;
+    int* h_steps = h_offsets + requests + 1;
+    int* h_perm = (int*)host.data() + rows + (requests + 1) + 3 * (size_t)requests;
+    h_offsets[0] = 0;
+    for (int k = 0; k < requests; ++k) {
+        const int r = order[k], n = row_offsets[r + 1] - row_offsets[r];
+        h_offsets[k + 1] = h_offsets[k] + n;
+        h_steps[k] = steps[r];
+        for (int i = 0; i < n; ++i) {
+            h_row_req[h_offsets[k] + i] = k;
+            h_perm[h_offsets[k] + i] = row_offsets[r] + i;
+        }
+    }
     int st = PCD_SUCCESS;
     hipError_t e = hipMemcpyAsync(tables, host.data(), tbytes, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess)
-        e = hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0_packed, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, rows,
-                             hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) {
+        if (identity) {
+            e = hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0_packed, (size_t)m->s[0] * 4,
+                                 (size_t)m->s[0] * 4, rows, hipMemcpyDeviceToDevice, s);
+        } else {
+            const int grid = (int)std::min<size_t>(((size_t)rows * m->s[0] + 255) / 256, 4096);
+            hipLaunchKernelGGL(permute_rows_kernel, dim3(grid), dim3(256), 0, s, x0_packed, m->s[0], w->M[0],
+                               m->P[0], (const int*)d_perm, rows, m->s[0], 1);
+            e = hipGetLastError();
+        }
+    }
     if (e != hipSuccess) st = from_hip(e, "ragged upload");
     if (!st) {
         RelaxSpec r;
@@ -1432,15 +1466,30 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
             }
         }
     }
-    if (!st) st = copy_out_rows(out_top, m->s[L - 1], w->M[L - 1], m->P[L - 1], rows, s);
+    if (!st) {
+        if (identity) {
+            st = copy_out_rows(out_top, m->s[L - 1], w->M[L - 1], m->P[L - 1], rows, s);
+        } else {
+            const int grid = (int)std::min<size_t>(((size_t)rows * m->s[L - 1] + 255) / 256, 4096);
+            hipLaunchKernelGGL(permute_rows_kernel, dim3(grid), dim3(256), 0, s, (const float*)w->M[L - 1],
+                               m->P[L - 1], out_top, m->s[L - 1], (const int*)d_perm, rows, m->s[L - 1], 0);
+            st = from_hip(hipGetLastError(), "permute_rows_kernel launch");
+        }
+    }
+    std::vector<int> used(requests);
     std::vector<float> last(requests);
     if (!st) {
-        e = hipMemcpyAsync(steps_used, d_done, (size_t)requests * 4, hipMemcpyDeviceToHost, s);
+        e = hipMemcpyAsync(used.data(), d_done, (size_t)requests * 4, hipMemcpyDeviceToHost, s);
         if (e == hipSuccess) e = hipMemcpyAsync(last.data(), d_last, (size_t)requests * 4, hipMemcpyDeviceToHost, s);
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e != hipSuccess) st = from_hip(e, "ragged download");
     }
-    if (!st && out_energy) std::memcpy(out_energy, last.data(), (size_t)requests * 4);
+    if (!st) {
+        for (int k = 0; k < requests; ++k) {
+            steps_used[order[k]] = used[k];
+            if (out_energy) out_energy[order[k]] = last[k];
+        }
+    }
     if (st) (void)hipStreamSynchronize(s);   // the upload reads `host` until the stream reaches it
     return st;
 }

@@ -297,6 +297,42 @@ def test_two_threads_on_two_streams_share_one_model():
         m.close()
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_ragged_budget_order_matches_caller_order(oracle, dtype):
+    # Settling the requests in decreasing budget (the default) permutes rows on
+    # the device and back: per request the same steps used, energies and top
+    # states as the caller's order (bit for bit in fp32, whose rows are
+    # independent; 16-bit models keep the K stagger, whose sum order follows
+    # the row tile, so those are held to the 16-bit bound).
+    from predicitivecoding_amd import PcDeviceModel
+    sizes = [40, 64, 32, 8]
+    snap, W, b, P, _ = build_case(sizes, "tanh", 0.1, seed=37)
+    rng = np.random.default_rng(11)
+    counts = [5, 70, 1, 33, 9, 64, 2, 17]
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    x = (rng.standard_normal((offs[-1], sizes[0])) * 0.3).astype(np.float32)
+    steps = np.array([4, 31, 9, 31, 2, 18, 25, 7], np.int32)
+    out = {}
+    for order in (0, 1):
+        m = PcDeviceModel(snap, dtype)
+        try:
+            m.set_option("ragged_order", order)
+            out[order] = [m.relax_ragged(x, offs, steps, rule, thr) for rule, thr in [("none", 0.0), ("absolute", 0.8)]]
+        finally:
+            m.close()
+    for (u0, e0, t0), (u1, e1, t1) in zip(out[0], out[1]):
+        assert np.array_equal(u0, u1)
+        if dtype == "f32":
+            assert np.array_equal(e0, e1) and np.array_equal(t0, t1)
+        else:
+            assert max_rel(e1, e0) < 2e-3 and max_rel(t1, t0) < 2e-3
+    if dtype == "f32":
+        used, fe, top = out[1][1]
+        rused, rfe, rtop = oracle.ragged_relax(sizes, "tanh", 0.1, W, b, P, x, offs, steps, "absolute", 0.8)
+        assert np.array_equal(used, rused)
+        assert max_rel(top, rtop) < 1e-4 and max_rel(fe, rfe) < 1e-4
+
+
 def test_ragged_graph_matches_eager_and_takes_new_tables(oracle):
     # The ragged loop replays a cached graph for calls of one shape (rows,
     # requests, longest budget, exit rule and threshold); each call's own
