@@ -284,6 +284,10 @@ def bench_ragged(args, cfg):
     apply_options(model, args)
     if args.tile_order >= 0:
         model.set_option("tile_order", args.tile_order)
+    if args.tile:
+        model.set_option("tile", args.tile)
+        if args.tile_n:
+            model.set_option("tile_n", args.tile_n)
     g = torch.Generator(device="cuda").manual_seed(1)
     x = torch.randn((rows, sizes[0]), generator=g, device="cuda", dtype=torch.float32)
     top = torch.empty((rows, sizes[-1]), device="cuda", dtype=torch.float32)
