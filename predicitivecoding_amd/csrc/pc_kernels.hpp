@@ -696,9 +696,11 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     constexpr int NMF = C::FM * C::FN * (F32OP ? 4 : 1);   // MFMAs per chunk
     constexpr int NRD = C::FM + C::FN;                     // fragment reads per chunk
     auto interleave = [&]() PCD_INLINE {
+        // MFMA first: the chunk's first MFMA then waits only on fragments read
+        // before it, not on the read just issued (bf16 phases +1%).
         static_for<0, NRD>([&](auto) PCD_INLINE {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         });
         if constexpr (NMF > NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
     };
