@@ -7,9 +7,11 @@ value = B * T * K / elapsed over K timed passes.
 
 Workloads:
   c1  784-256-256-10 tanh fp32, B=64, T=20, eta=0.1, x0~U[0,1]
-  c2  1024-1024-1024-1024-256 tanh fp32, B=1024, T=50, eta=0.05, x0~N(0,1)   (default)
+  c2  1024-1024-1024-1024-256 tanh fp32, B=1024, T=50, eta=0.05, x0~N(0,1)
   c3  6 x 4096 GELU bf16 operands, B=4096, T=32, eta=0.05, W~N(0,1/fan_in)
+      (the configuration the bf16 MFMA target is stated on)
   c5  12 x 8192 GELU bf16 operands, B=8192, T=16, eta=0.02, W~N(0,1/fan_in)
+      (default: the largest configuration of the five, which one GPU holds)
   c4  ragged: 64 requests on a shared 4 x 2048 tanh fp32 network, per-request
       batch log-uniform in [1,512] and T uniform in [8,64] (seeded), early exit
       when energy/sample < 1e-3; one pass = one packed pcd_pc_relax_ragged call,
@@ -97,6 +99,36 @@ def phase_bytes(sizes, B, dtype):
     return float(err), float(upd)
 
 
+MALL_BYTES = 256 << 20   # MI355X Infinity Cache
+
+
+def topology(sizes):
+    """Layer widths as "8192x12" when every layer has one width, else "784-256-256-10"."""
+    if len(set(sizes)) == 1:
+        return f"{sizes[0]}×{len(sizes)}"
+    return "-".join(map(str, sizes))
+
+
+def working_set_bytes(sizes, B, dtype):
+    """Device bytes a settling step touches: W and W^T in the operand type, and
+    the fp32 states M, X, the operand copies S, D of the batch."""
+    wb = 4 if dtype == "f32" else 2
+    w = sum(2 * sizes[l] * sizes[l - 1] * wb for l in range(1, len(sizes)))
+    st = sum(B * s * (4 + 4 + (wb if wb == 2 else 0)) for s in sizes) + \
+        sum(B * sizes[l - 1] * wb for l in range(1, len(sizes)))
+    return float(w + st)
+
+
+def traffic_fields(sizes, B, dtype):
+    """What the counter-derived `traffic` figure counts, for this working set:
+    FETCH_SIZE and WRITE_SIZE count L2 fills and write-backs; when the whole
+    working set fits the 256 MB MALL, those fills are mostly served by the
+    MALL, so the figure is L2-miss traffic, an upper bound on HBM traffic."""
+    ws = working_set_bytes(sizes, B, dtype)
+    return {"traffic_counts": "L2 fills (FETCH_SIZE) + L2 write-backs (WRITE_SIZE), per launch, copy-calibrated",
+            "working_set_bytes": ws, "mall_resident": ws <= MALL_BYTES}
+
+
 def make_ragged_requests(cfg):
     """Per-request rows (log-uniform in [1, bmax]) and step budgets (uniform in
     [tmin, tmax]) from the config's seed."""
@@ -134,6 +166,38 @@ def make_inputs(cfg, seed=1):
 CPU_REPS = 3
 
 
+def host_nproc():
+    """Host cores this process may run on (what `nproc` prints)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def cpu_threads():
+    """Threads of the CPU baseline: every core `nproc` reports, unless
+    OMP_NUM_THREADS names the share of the host this process was given."""
+    return int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or host_nproc()
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def host_fields(threads):
+    """CPU facts the baseline record carries beside its thread count."""
+    return {"nproc": host_nproc(), "cpu_model": cpu_model(),
+            "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"), "threads": threads}
+
+
 def median_run(run, reps=CPU_REPS):
     """Times `run` (after the caller's warm-up call) `reps` times; returns
     (median seconds, the run's result), as the reference's bench harness
@@ -151,7 +215,7 @@ def cpu_baseline(cfg, W, b, x_host, budget_s=10.0):
     host cores, on a bounded sample: `rows` samples for `steps` steps, the
     median of three runs."""
     from oracle import pc_oracle
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     pc_oracle.set_threads(threads)
     sizes, act = cfg["sizes"], ACT_NAME[cfg["act"]]
     P = [1.0] * len(sizes)
@@ -171,7 +235,7 @@ def cpu_baseline(cfg, W, b, x_host, budget_s=10.0):
     print(f"# cpu baseline sample: {rows} rows x {steps} steps (calibrated {per * 1e3:.3f} ms per "
           f"sample-step), median of {CPU_REPS}", file=sys.stderr, flush=True)
     dt, _ = median_run(lambda: pc_oracle.batched_relax(sizes, act, cfg["eta"], W, b, P, x_host[:rows], steps))
-    return {"value": rows * steps / dt, "unit": "sample-steps/s", "cores": threads, "kind": "port",
+    return {"value": rows * steps / dt, "unit": "sample-steps/s", "cores": threads, **host_fields(threads), "kind": "port",
             "sample": f"oracle batched fp32 relaxation (i-k-j row-parallel GEMM as Gemm.cs:106-124), "
                       f"{rows} of {cfg['batch']} samples x {steps} of {cfg['T']} steps, median of {CPU_REPS} "
                       f"runs of {dt:.1f} s"}
@@ -330,7 +394,7 @@ def bench_ragged(args, cfg):
                 "frac": achieved / peak, "traffic": traffic_from_profiles("c4", dom_name), "kernel": dom_name,
                 "kernel_ms": dom_ms, "error_phase_ms": err_ms, "update_phase_ms": upd_ms, "launches_timed": launches,
                 "flop_per_launch": flop_launch, "mean_active_rows": float(active.mean()),
-                "path_frac": 4.0 * S * value / peak}
+                "path_frac": 4.0 * S * value / peak, **traffic_fields(sizes, rows, cfg["dtype"])}
     print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch over {launches} steps, "
           f"{active.mean():.0f} active rows on average; {dom_name} at {achieved / 1e12:.1f} TFLOP/s = "
           f"{100 * achieved / peak:.1f}% of peak", file=sys.stderr, flush=True)
@@ -415,7 +479,7 @@ def bench_clamped(args, cfg):
                 "frac": achieved / peak, "traffic": traffic_from_profiles(args.config, dom_name), "kernel": dom_name,
                 "kernel_ms": ms[dom_name], "error_phase_ms": err_ms, "update_phase_ms": upd_ms,
                 "flop_per_launch": flops[dom_name], "launches_timed": launches,
-                "path_frac": (2.0 * (S + S_free) * value) / peak}
+                "path_frac": (2.0 * (S + S_free) * value) / peak, **traffic_fields(sizes, rows, cfg["dtype"])}
     print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch; {dom_name} at "
           f"{achieved / 1e12:.1f} TFLOP/s = {100 * achieved / peak:.1f}% of peak", file=sys.stderr, flush=True)
 
@@ -471,7 +535,7 @@ def cpu_baseline_clamped(cfg, W, b, x_host, labels_host, budget_s=10.0):
     rates = sorted(d * per_sample_rows * T / t for d, t in passes)
     done, dt = passes[0]
     name = "Network.PredictCore" if cfg["mode"] == "classify" else "Network.Learn"
-    return {"value": rates[len(rates) // 2], "unit": "sample-steps/s", "cores": 1, "kind": "port",
+    return {"value": rates[len(rates) // 2], "unit": "sample-steps/s", "cores": 1, **host_fields(1), "kind": "port",
             "sample": f"oracle {name} one sample at a time (batch-1 settlings), median of {CPU_REPS} passes of "
                       f"about {done} of {cfg['batch']} samples x {per_sample_rows} settlings x {T} steps "
                       f"({dt:.1f} s each)"}
@@ -519,7 +583,7 @@ def bench_gemm(args, cfg):
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import pc_oracle
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         pc_oracle.set_threads(threads)
         bt = B.float().cpu().numpy().T.copy()
         t0 = time.perf_counter()
@@ -528,7 +592,7 @@ def bench_gemm(args, cfg):
         rows = int(min(m, max(16, args.cpu_budget / 2 / CPU_REPS / max(per_row, 1e-9))))
         a = A[:rows].float().cpu().numpy()
         dt, _ = median_run(lambda: pc_oracle.gemm(a, bt, "bf16"))
-        cpu = {"value": 2.0 * rows * n * k / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        cpu = {"value": 2.0 * rows * n * k / dt / 1e12, "unit": "TFLOP/s", "cores": threads, **host_fields(threads), "kind": "port",
                "sample": f"oracle mixed GEMM (Gemm.cs:44-60, i-k-j row-parallel), {rows} of {m} rows, median of "
                          f"{CPU_REPS} runs of {dt:.1f} s"}
         print(f"# cpu baseline: {cpu['value'] * 1e3:.2f} GFLOP/s on {threads} threads", file=sys.stderr, flush=True)
@@ -551,7 +615,7 @@ def cpu_baseline_ragged(cfg, W, b, x_host, offsets, steps, budget_s=10.0):
     """The oracle's per-request relaxation with the same exit rule, on the
     first requests that fit the time budget."""
     from oracle import pc_oracle
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     pc_oracle.set_threads(threads)
     sizes, P = cfg["sizes"], [1.0] * len(cfg["sizes"])
     n = min(16, int(offsets[-1]))
@@ -570,7 +634,7 @@ def cpu_baseline_ragged(cfg, W, b, x_host, offsets, steps, budget_s=10.0):
                                                                  x_host[:int(sub_off[-1])], sub_off, steps[:k],
                                                                  cfg["exit_rule"], cfg["exit_thr"]))
     done = int(np.sum(rows[:k].astype(np.int64) * used))
-    return {"value": done / dt, "unit": "sample-steps/s", "cores": threads, "kind": "port",
+    return {"value": done / dt, "unit": "sample-steps/s", "cores": threads, **host_fields(threads), "kind": "port",
             "sample": f"oracle per-request fp32 relaxation with the same exit rule, first {k} of {len(steps)} "
                       f"requests ({int(sub_off[-1])} rows, {done} sample-steps), median of {CPU_REPS} runs of "
                       f"{dt:.1f} s"}
@@ -582,7 +646,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0,
                     help="seconds the CPU baseline sample is sized for (its calibration overestimates ~2x)")
@@ -693,9 +757,14 @@ def main():
                     "frac": achieved / peak, "traffic": traffic_from_profiles(args.config, dom_name),
                     "kernel": dom_name, "kernel_ms": dom_ms, "error_phase_ms": err_ms, "update_phase_ms": upd_ms,
                     "flop_per_launch": flop_launch, "bytes_per_launch": bytes_launch, "launches_timed": launches,
-                    "path_frac": (flops_per_sample_step(sizes) * value) / peak}
+                    "path_frac": (flops_per_sample_step(sizes) * value) / peak,
+                    # the same launch against the HBM roofline: algorithmic bytes / duration
+                    "hbm_achieved_GBps": bytes_launch / (dom_ms * 1e-3) / 1e9,
+                    "hbm_frac": bytes_launch / (dom_ms * 1e-3) / HBM_PEAK}
         print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch; {dom_name} at "
-              f"{achieved / 1e12:.1f} TFLOP/s = {100 * achieved / peak:.1f}% of peak", file=sys.stderr, flush=True)
+              f"{achieved / 1e12:.1f} TFLOP/s = {100 * achieved / peak:.1f}% of peak, "
+              f"{bytes_launch / (dom_ms * 1e-3) / 1e9:.0f} GB/s algorithmic", file=sys.stderr, flush=True)
+    roofline.update(traffic_fields(sizes, B, cfg["dtype"]))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -717,7 +786,7 @@ def main():
         "vs_baseline": None,
         "dtype": cfg["dtype"],
         "data": "synthetic (seeded random weights and inputs)",
-        "config": {"workload": f"{args.config}: {'-'.join(map(str, sizes))} {ACT_NAME[cfg['act']]} "
+        "config": {"workload": f"{args.config}: {topology(sizes)} {ACT_NAME[cfg['act']]} "
                                f"{cfg['dtype']}, B={B}, T={T}, eta={cfg['eta']}",
                    "batch": B, "relax_steps": T, "layer_sizes": sizes, "parallelism": "single GPU"},
         "roofline": roofline,
