@@ -81,6 +81,7 @@ struct Pool {
     };
     std::map<Key, std::vector<void*>> free_blocks;
     std::unordered_map<void*, std::pair<int, int>> live;  // ptr -> (device, bucket)
+    std::unordered_map<void*, bool> synchronous;          // blocks from the hipMalloc fallback (freed with hipFree)
     std::map<int, std::vector<void*>> host_free;          // bucket -> pinned blocks
     std::unordered_map<void*, int> host_live;
     static constexpr size_t kMaxCached = 32;
@@ -115,14 +116,17 @@ int pool_alloc(void** out, size_t bytes, hipStream_t stream) {
         }
     }
     void* p = nullptr;
+    bool fallback = false;
     hipError_t e = hipMallocAsync(&p, (size_t)1 << b, stream);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         e = hipMalloc(&p, (size_t)1 << b);  // CudaAllocator.cs:43-44 fallback
+        fallback = true;
     }
     if (e != hipSuccess) return from_hip(e, "pcd_malloc_async");
     std::lock_guard<std::mutex> g(P.mu);
     P.live[p] = {dev, b};
+    if (fallback) P.synchronous[p] = true;
     *out = p;
     return PCD_SUCCESS;
 }
@@ -138,6 +142,15 @@ int pool_free(void* ptr, hipStream_t stream) {
     auto& v = P.free_blocks[{dev, (void*)stream, b}];
     if (v.size() < Pool::kMaxCached) {
         v.push_back(ptr);
+        return PCD_SUCCESS;
+    }
+    // A block of the stream-ordered allocator goes back to it in stream order;
+    // one from the synchronous fallback must not be handed to hipFreeAsync.
+    auto fb = P.synchronous.find(ptr);
+    if (fb != P.synchronous.end()) {
+        P.synchronous.erase(fb);
+        HIP_TRY(hipStreamSynchronize(stream));   // the stream's queued work may still use it
+        HIP_TRY(hipFree(ptr));
         return PCD_SUCCESS;
     }
     HIP_TRY(hipFreeAsync(ptr, stream));
@@ -265,6 +278,17 @@ struct Plan {
     hipGraphExec_t exec = nullptr;
     hipGraph_t graph = nullptr;
     uint64_t last_use = 0;
+
+    Plan() = default;
+    Plan(const Plan&) = delete;
+    Plan& operator=(const Plan&) = delete;
+    // The owner makes sure no launch of the graph is still queued (it
+    // synchronises the stream the plan was launched on first).
+    ~Plan() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (energy_out) (void)hipFree(energy_out);
+    }
 };
 
 }  // namespace
@@ -294,12 +318,8 @@ struct pcd_model {
 
 namespace {
 
+// Callers have synchronised the workspace's stream (or the device).
 void free_workspace(Workspace& w) {
-    for (auto& p : w.plans) {
-        if (p->exec) (void)hipGraphExecDestroy(p->exec);
-        if (p->graph) (void)hipGraphDestroy(p->graph);
-        if (p->energy_out) (void)hipFree(p->energy_out);
-    }
     w.plans.clear();
     for (void* p : w.owned) (void)hipFree(p);
     w.owned.clear();
@@ -748,9 +768,11 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
     if (w->plans.size() >= 8) {  // evict the least recently used plan
         auto it = std::min_element(w->plans.begin(), w->plans.end(),
                                    [](const auto& a, const auto& b) { return a->last_use < b->last_use; });
-        if ((*it)->exec) (void)hipGraphExecDestroy((*it)->exec);
-        if ((*it)->graph) (void)hipGraphDestroy((*it)->graph);
-        if ((*it)->energy_out) (void)hipFree((*it)->energy_out);
+        // Its last launch may still be queued on the workspace's stream (the
+        // relax calls return without waiting): let it finish before the
+        // executable graph and its energy buffer go.
+        hipError_t e = hipStreamSynchronize(w->stream);
+        if (e != hipSuccess) { *status = from_hip(e, "hipStreamSynchronize (plan eviction)"); return nullptr; }
         w->plans.erase(it);
     }
     std::unique_ptr<Plan> p(new Plan());
@@ -763,7 +785,7 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
     p->exit_rule = requests ? r.exit_rule : 0;
     p->exit_thr = requests ? r.exit_thr : 0.f;
     p->last_use = ++m->clock;
-    if (want_energy) {
+    if (want_energy) {   // on any failure below, ~Plan releases what was made
         hipError_t e = hipMalloc(&p->energy_out, (size_t)r.steps * r.batch * 4);
         if (e != hipSuccess) { *status = from_hip(e, "hipMalloc(energy)"); return nullptr; }
     }
@@ -816,6 +838,17 @@ int run_relax(pcd_model* m, Workspace* w, int batch, int steps, int clamp_top, i
     if (!p) return st;
     HIP_TRY(hipGraphLaunch(p->exec, s));
     *energy = p->energy_out;
+    return PCD_SUCCESS;
+}
+
+// Drops every cached graph of the model, once the streams that may still be
+// running one of them have drained.
+int drop_plans(pcd_model* m) {
+    for (auto& w : m->ws) {
+        if (w->plans.empty()) continue;
+        HIP_TRY(hipStreamSynchronize(w->stream));
+        w->plans.clear();
+    }
     return PCD_SUCCESS;
 }
 
@@ -923,7 +956,10 @@ int pcd_trim_pools(void) {
     Pool& P = pool();
     std::lock_guard<std::mutex> g(P.mu);
     for (auto& kv : P.free_blocks)
-        for (void* p : kv.second) (void)hipFree(p);
+        for (void* p : kv.second) {
+            (void)hipFree(p);
+            P.synchronous.erase(p);
+        }
     P.free_blocks.clear();
     for (auto& kv : P.host_free)
         for (void* p : kv.second) (void)hipHostFree(p);
@@ -1291,15 +1327,7 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
         m->k_stagger = value;
     } else return fail(PCD_INVALID_VALUE, "unknown option '%s'", name);
     // cached graphs were captured with the old options
-    for (auto& w : m->ws) {
-        for (auto& p : w->plans) {
-            if (p->exec) (void)hipGraphExecDestroy(p->exec);
-            if (p->graph) (void)hipGraphDestroy(p->graph);
-            if (p->energy_out) (void)hipFree(p->energy_out);
-        }
-        w->plans.clear();
-    }
-    return PCD_SUCCESS;
+    return drop_plans(m);
 }
 
 int pcd_pc_profile_result(pcd_model* m, float* err_ms, float* upd_ms, int* launches) {
@@ -1851,15 +1879,7 @@ int pcd_pc_model_load_record(pcd_model* m, int layer, const void* record, size_t
     if (e != hipSuccess) return from_hip(e, "pcd_pc_model_load_record");
     m->prec[layer] = r.precision;
     // cached graphs carry the precisions in their launch arguments
-    for (auto& w : m->ws) {
-        for (auto& p : w->plans) {
-            if (p->exec) (void)hipGraphExecDestroy(p->exec);
-            if (p->graph) (void)hipGraphDestroy(p->graph);
-            if (p->energy_out) (void)hipFree(p->energy_out);
-        }
-        w->plans.clear();
-    }
-    return PCD_SUCCESS;
+    return drop_plans(m);
 }
 
 
