@@ -25,13 +25,26 @@ from .errors import ArgumentException, ArgumentNullException, ArgumentOutOfRange
 from .snapshot import GenerativeSnapshot
 
 
+def _check_ragged_tables(offs: np.ndarray, steps: np.ndarray) -> None:
+    """Host tables of a ragged call: R >= 1 requests, R + 1 strictly increasing
+    row offsets from 0 (the library reads row_offsets[R]), budgets >= 1."""
+    R = len(steps)
+    if R < 1:
+        raise ArgumentException("Empty batch.")
+    if len(offs) != R + 1 or offs[0] != 0 or np.any(np.diff(offs) < 1):
+        raise ArgumentException("row_offsets must start at 0, increase strictly and end at the row count")
+    if np.any(steps < 1):
+        raise ArgumentOutOfRangeException("steps")
+
+
 class PcDeviceModel:
     """A GenerativeSnapshot uploaded to the current GPU in one operand dtype."""
 
     def __init__(self, snapshot: GenerativeSnapshot, dtype: str = "f32"):
         if dtype not in DTYPE:
             raise ArgumentException(f"dtype must be one of {sorted(DTYPE)}")
-        self.snapshot = snapshot
+        # the weights are copied to the device: no reference to the snapshot
+        # is kept (the drop-in's cache frees a model when its snapshot dies)
         self.dtype = dtype
         L = len(snapshot.layer_sizes)
         self.sizes = list(snapshot.layer_sizes)
@@ -111,6 +124,7 @@ class PcDeviceModel:
         offs = np.ascontiguousarray(row_offsets, dtype=np.int32)
         st = np.ascontiguousarray(steps, dtype=np.int32)
         R = len(st)
+        _check_ragged_tables(offs, st)
         used = np.zeros(R, dtype=np.int32)
         fe = np.zeros(R, dtype=np.float32)
         if exit_rule not in EXIT:
@@ -128,12 +142,9 @@ class PcDeviceModel:
         offs = np.ascontiguousarray(row_offsets, dtype=np.int32)
         st = np.ascontiguousarray(steps, dtype=np.int32)
         R = len(st)
-        if R < 1:
-            raise ArgumentException("Empty batch.")
-        if len(offs) != R + 1 or offs[0] != 0 or np.any(np.diff(offs) < 1) or offs[-1] != x0.shape[0]:
+        _check_ragged_tables(offs, st)
+        if offs[-1] != x0.shape[0]:
             raise ArgumentException("row_offsets must start at 0, increase strictly and end at the row count")
-        if np.any(st < 1):
-            raise ArgumentOutOfRangeException("steps")
         if exit_rule not in EXIT:
             raise ArgumentException(f"exit_rule must be one of {sorted(EXIT)}")
         rows = int(offs[-1])
@@ -268,7 +279,6 @@ class PcDeviceModel:
         sizes = [struct.unpack_from("<i", r, 0)[0] for r in records]
         precisions = [struct.unpack_from("<f", r, 8)[0] for r in records]
         self = cls.__new__(cls)
-        self.snapshot = None
         self.dtype = dtype
         self.sizes = sizes
         L = len(sizes)
@@ -295,8 +305,22 @@ class PcDeviceModel:
         return W, b
 
 
+def _release_cached(key) -> None:
+    """Drops a snapshot's device model from the drop-in's cache and frees it
+    (W, W^T, workspaces, cached graphs); runs when the snapshot is collected."""
+    hit = BatchedPcForward._cache.pop(key, None)
+    if hit is not None:
+        hit[1].close()
+
+
 class BatchedPcForward:
-    """Drop-in for the reference's static class (BatchedPcForward.cs:28-139)."""
+    """Drop-in for the reference's static class (BatchedPcForward.cs:28-139).
+
+    The reference transposes and uploads nothing it keeps: every call starts
+    from the snapshot.  Here a snapshot's weights are uploaded once per operand
+    type and kept on the device while the snapshot lives; the device model is
+    freed when the snapshot is collected (a weakref finalizer), so a caller
+    that makes snapshot after snapshot holds at most the live ones."""
 
     _cache: dict = {}
 
@@ -306,9 +330,17 @@ class BatchedPcForward:
         hit = BatchedPcForward._cache.get(key)
         if hit is not None and hit[0]() is snapshot:
             return hit[1]
+        if hit is not None:          # an id reused by a newer object: the old model is stale
+            _release_cached(key)
         m = PcDeviceModel(snapshot, dtype)
         BatchedPcForward._cache[key] = (weakref.ref(snapshot), m)
+        weakref.finalize(snapshot, _release_cached, key)
         return m
+
+    @staticmethod
+    def cached_models() -> int:
+        """Device models the drop-in currently holds (one per live snapshot and operand type)."""
+        return len(BatchedPcForward._cache)
 
     @staticmethod
     def infer_get_top_batch(model: GenerativeSnapshot, inputs, inference_steps: int, mixed: bool = False,

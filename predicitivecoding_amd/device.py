@@ -123,7 +123,11 @@ class Event:
             pass
 
 
-_NP_DTYPES = {np.dtype(np.float32), np.dtype(np.uint16), np.dtype(np.int32)}
+# float16 tensors hold fp16 GEMM operands; uint16 tensors hold raw bf16 bit
+# patterns (numpy has no bfloat16).
+_NP_DTYPES = {np.dtype(np.float32), np.dtype(np.float16), np.dtype(np.uint16), np.dtype(np.int32)}
+_GEMM_FN = {np.dtype(np.float32): "pcd_gemm_f32", np.dtype(np.float16): "pcd_gemm_f16",
+            np.dtype(np.uint16): "pcd_gemm_bf16"}
 
 
 class DeviceTensor:
@@ -183,16 +187,22 @@ class TensorOps:
     @staticmethod
     def mat_mul(a: DeviceTensor, b: DeviceTensor, trans_a: bool = False, trans_b: bool = False,
                 beta: float = 0.0, out: DeviceTensor | None = None, stream: Stream | None = None) -> DeviceTensor:
-        """Row-major C = op(A) op(B) + beta C in fp32 (MatMulDeviceEx semantics)."""
+        """Row-major C = op(A) op(B) + beta C with an fp32 C (MatMulDeviceEx
+        semantics): fp32 operands, fp16 operands (float16 tensors,
+        MatMulMixedDevice) or bf16 operands (uint16 tensors of bf16 bits,
+        MatMulDeviceExBf16).  Both operands must have the same type."""
         if len(a.shape) != 2 or len(b.shape) != 2:
             raise ArgumentException("MatMul needs 2-D tensors")
+        if a.dtype != b.dtype or a.dtype not in _GEMM_FN:
+            raise ArgumentException(f"MatMul operands must share one of float32, float16 or uint16 (bf16); "
+                                    f"got {a.dtype} and {b.dtype}")
         m, k = (a.shape[1], a.shape[0]) if trans_a else a.shape
         k2, n = (b.shape[1], b.shape[0]) if trans_b else b.shape
         if k != k2:
             raise ArgumentException(f"inner dimensions differ: {k} vs {k2}")
         if out is None:
             out = DeviceTensor((m, n), np.float32, stream)
-        fn = {np.dtype(np.float32): "pcd_gemm_f32", np.dtype(np.uint16): "pcd_gemm_bf16"}[a.dtype]
+        fn = _GEMM_FN[a.dtype]
         call(fn, a.ptr, b.ptr, out.ptr, m, k, n, int(trans_a), int(trans_b), float(beta),
              stream.handle if stream else None)
         if stream is None:

@@ -1,0 +1,119 @@
+"""The reference-API drop-in, BatchedPcForward.infer_get_top_batch, on the GPU.
+
+Mirrors PredicitiveCoding.UnitTests/BatchedPcForwardTests.cs: the [6,10,4]
+tanh network (eta 0.1, eta_w 0.05) trained on two patterns, inputs uniform in
+[-1, 1], and the reference's bounds |a-b| <= tol*(1+|b|):
+  batched == per-sample InferGetTop          1e-3   (:44-72, :74-92 with FFG)
+  mixed tracks float                          5e-2   (:94-111)
+and, tighter, this build's own bars: fp32 against the fp32 oracle 1e-4, and
+16-bit operands against the oracle with the same operand rounding 2e-3.
+"""
+import gc
+
+import numpy as np
+import pytest
+
+from tests.netgen import close, make_inputs, make_net, max_rel
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [6, 10, 4]
+
+
+def _trained_snapshot(oracle, seed, ffg=False):
+    """The reference test's network: Xavier-normal weights, then 30 rounds of
+    Learn(x0 = 0 -> class 0) and Learn(x1 = 1 -> class 1) with 10 steps
+    (BatchedPcForwardTests.cs:47-56), here with the oracle's learning step."""
+    from predicitivecoding_amd import GenerativeSnapshot
+    W, b, P = make_net(SIZES, seed=seed)
+    x0, x1 = np.zeros((1, 6), np.float32), np.ones((1, 6), np.float32)
+    y0, y1 = np.eye(4, dtype=np.float32)[:1], np.eye(4, dtype=np.float32)[1:2]
+    for _ in range(30):
+        for x, y in ((x0, y0), (x1, y1)):
+            W, b, _ = oracle.learn(SIZES, "tanh", 0.1, W, b, P, x, y, 10, 0.05)
+    W = [np.ascontiguousarray(w, np.float32) for w in W]
+    b = [np.ascontiguousarray(v, np.float32) for v in b]
+    return GenerativeSnapshot(SIZES, 1, 0.1, 0.0, ffg, W, b, list(P)), W, b, P
+
+
+def _inputs(count, seed):
+    return [row for row in make_inputs(count, 6, seed=seed, dist="uniform11")]
+
+
+def test_batch_matches_per_sample_infer_get_top(oracle):
+    from predicitivecoding_amd import BatchedPcForward
+    snap, W, b, P = _trained_snapshot(oracle, seed=0)
+    inputs = _inputs(5, seed=3)
+    batched = BatchedPcForward.infer_get_top_batch(snap, inputs, 15)
+    assert len(batched) == 5 and all(t.shape == (4,) and t.dtype == np.float32 for t in batched)
+    got = np.stack(batched)
+    x = np.stack(inputs)
+    per_sample, _, _ = oracle.persample_relax_f64(SIZES, "tanh", 0.1, W, b, P, x, 15)
+    ref32, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, W, b, P, x, 15)
+    print(f"drop-in fp32: vs per-sample f64 {max_rel(got, per_sample):.2e}, vs oracle {max_rel(got, ref32):.2e}",
+          flush=True)
+    assert close(got, per_sample, 1e-3)
+    assert max_rel(got, ref32) < 1e-4
+
+
+def test_batch_with_feedforward_gist_matches_per_sample(oracle):
+    from predicitivecoding_amd import BatchedPcForward, GenerativeSnapshot
+    W, b, P = make_net(SIZES, seed=1)
+    snap = GenerativeSnapshot(SIZES, 1, 0.1, 0.0, True, W, b, list(P))
+    inputs = _inputs(4, seed=5)
+    got = np.stack(BatchedPcForward.infer_get_top_batch(snap, inputs, 10))
+    x = np.stack(inputs)
+    per_sample, _, _ = oracle.persample_relax_f64(SIZES, "tanh", 0.1, W, b, P, x, 10, ffg=True)
+    ref32, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, W, b, P, x, 10, ffg=True)
+    assert close(got, per_sample, 1e-3)
+    assert max_rel(got, ref32) < 1e-4
+
+
+@pytest.mark.parametrize("dtype", [None, "bf16"])
+def test_mixed_batch_tracks_float_batch(oracle, dtype):
+    # mixed=True is fp16 operands (Gemm.cs:44-60); dtype="bf16" selects bf16
+    from predicitivecoding_amd import BatchedPcForward
+    snap, W, b, P = _trained_snapshot(oracle, seed=2)
+    inputs = _inputs(4, seed=7)
+    full = np.stack(BatchedPcForward.infer_get_top_batch(snap, inputs, 15))
+    mixed = np.stack(BatchedPcForward.infer_get_top_batch(snap, inputs, 15, mixed=True, dtype=dtype))
+    x = np.stack(inputs)
+    same, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, W, b, P, x, 15, round_mode=dtype or "f16")
+    print(f"drop-in mixed/{dtype or 'f16'}: vs float {max_rel(mixed, full):.2e}, "
+          f"vs same rounding {max_rel(mixed, same):.2e}", flush=True)
+    assert close(mixed, full, 5e-2)
+    assert max_rel(mixed, same) < 2e-3
+    assert not np.array_equal(mixed, full)   # the 16-bit path really ran
+
+
+def test_drop_in_releases_device_models_with_their_snapshots(oracle):
+    # The drop-in keeps one device model per live snapshot and operand type;
+    # a snapshot that is collected takes its model (W, W^T, workspaces,
+    # graphs) with it, so a caller exporting snapshot after snapshot does not
+    # accumulate device memory.
+    from predicitivecoding_amd import BatchedPcForward, GenerativeSnapshot
+    gc.collect()
+    base = BatchedPcForward.cached_models()
+    inputs = _inputs(3, seed=9)
+    keep = None
+    for k in range(6):
+        W, b, P = make_net(SIZES, seed=40 + k)
+        snap = GenerativeSnapshot(SIZES, 1, 0.1, 0.0, False, W, b, list(P))
+        top = np.stack(BatchedPcForward.infer_get_top_batch(snap, inputs, 5))
+        ref, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, W, b, P, np.stack(inputs), 5)
+        assert max_rel(top, ref) < 1e-4
+        if k == 0:
+            keep = snap
+            BatchedPcForward.infer_get_top_batch(snap, inputs, 5, mixed=True)
+        del snap
+        gc.collect()
+        assert BatchedPcForward.cached_models() == base + 2   # keep's f32 and f16 models only
+    # the kept snapshot's models are still the cached ones and still work
+    again = np.stack(BatchedPcForward.infer_get_top_batch(keep, inputs, 5))
+    assert BatchedPcForward.cached_models() == base + 2
+    W, b, P = make_net(SIZES, seed=40)
+    ref, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, W, b, P, np.stack(inputs), 5)
+    assert max_rel(again, ref) < 1e-4
+    del keep
+    gc.collect()
+    assert BatchedPcForward.cached_models() == base
