@@ -97,3 +97,69 @@ def autograd_learn(sizes, act, eta, W, b, prec, x0, labels, steps, eta_w, weight
         new_w.append(w)
         new_b.append(bb)
     return new_w, new_b, energies[-1]
+
+
+ROUND_POINTS = ("state", "wt", "delta", "w")
+
+
+def _round16(x, mode):
+    """Round-to-nearest-even to bf16 or fp16 of the fp32 value of x (torch's
+    own conversions), carried on in float64."""
+    if mode == "bf16":
+        return x.float().to(torch.bfloat16).double()
+    return x.float().to(torch.float16).double()
+
+
+def mixed_relax_f64(sizes, act, eta, W, b, prec, x0, steps, mode, drop=()):
+    """The batched relaxation with 16-bit GEMM operands, stated directly in
+    float64: every operation in float64 except that both operands of both
+    GEMMs are rounded to `mode` where BatchedPcForward's mixed path rounds them
+    (Gemm.cs:44-60 rounds A and B of every MatMulMixed call):
+        pre_l = round(M_l) round(W_l)^T + b_l            (TopDown, :74-80)
+        G_l   = round(f'(pre_l) * e_{l-1}) round(W_l)     (Mul(delta, W_l), :117)
+    The weights never change during a settling, so rounding them once equals
+    rounding them per call.  `drop` names rounding points to leave out
+    ("state", "wt", "delta", "w"): each one left out moves the result by far
+    more than the fp32-versus-float64 difference, which is how a test shows
+    that this statement pins every point.  Returns (top, energies [T, B])."""
+    f = _act(act)
+    fprime = _act_deriv(act)
+    dt = torch.float64
+    L = len(sizes)
+    R = lambda x, point: x if point in drop else _round16(x, mode)
+    Wt = [torch.tensor(np.asarray(w, dtype=np.float64), dtype=dt) for w in W]
+    W_g2 = [R(w, "w") for w in Wt]               # GEMM 2's B operand, W_l
+    W_g1 = [R(w.T.contiguous(), "wt") for w in Wt]  # GEMM 1's B operand, W_l^T
+    bt = [torch.tensor(np.asarray(v, dtype=np.float64), dtype=dt) for v in b]
+    P = [float(p) for p in prec]
+    x = torch.tensor(np.asarray(x0, dtype=np.float64), dtype=dt)
+    B = x.shape[0]
+    mu = [x] + [torch.zeros(B, s, dtype=dt) for s in sizes[1:]]
+    energies = np.zeros((steps, B))
+    for t in range(steps):
+        pre = [None] + [R(mu[l], "state") @ W_g1[l - 1] + bt[l - 1] for l in range(1, L)]
+        e = [P[l] * (mu[l] - f(pre[l + 1])) for l in range(L - 1)] + [torch.zeros(B, sizes[-1], dtype=dt)]
+        energies[t] = sum(0.5 * (e[l] * e[l]).sum(dim=1) / P[l] for l in range(L - 1)).numpy()
+        new = [mu[0]]
+        for l in range(1, L):
+            delta = fprime(pre[l]) * e[l - 1]
+            g = R(delta, "delta") @ W_g2[l - 1]
+            new.append(mu[l] - eta * (e[l] - g))
+        mu = new
+    return mu[-1].numpy(), energies
+
+
+def _act_deriv(name):
+    """f'(pre) in closed form, as Activation.cs:86-132 and Autograd.cs:313-318
+    state them (tanh from the output, GELU-tanh from the pre-activation)."""
+    def gelu_d(x):
+        c, a = 0.7978845608028654, 0.044715
+        t = torch.tanh(c * (x + a * x ** 3))
+        return 0.5 * (1 + t) + 0.5 * x * (1 - t * t) * c * (1 + 3 * a * x * x)
+    return {
+        "linear": lambda x: torch.ones_like(x),
+        "tanh": lambda x: 1 - torch.tanh(x) ** 2,
+        "relu": lambda x: (x > 0).to(x.dtype),
+        "sigmoid": lambda x: torch.sigmoid(x) * (1 - torch.sigmoid(x)),
+        "gelu": gelu_d,
+    }[name]

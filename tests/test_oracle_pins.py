@@ -279,6 +279,39 @@ def test_mixed_tracks_float(oracle, mode):
     assert not np.array_equal(mixed, full)
 
 
+def _rel_rms(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.sqrt(np.mean((a - b) ** 2)) / np.sqrt(np.mean(b ** 2)))
+
+
+@pytest.mark.parametrize("mode", ["bf16", "f16"])
+@pytest.mark.parametrize("act", ["tanh", "gelu"])
+def test_mixed_rounding_points_against_float64_statement(oracle, mode, act):
+    # The oracle's 16-bit relaxation (W and W^T rounded once, the state and
+    # delta operands rounded at every GEMM, Gemm.cs:44-60 as BatchedPcForward
+    # calls it) against an independent float64 torch statement that rounds the
+    # same four operands (tests/autograd_ref.py:mixed_relax_f64).  Rare
+    # rounding-boundary flips (fp32 and float64 values on either side of a
+    # 16-bit midpoint) keep the two from agreeing bit for bit, so the
+    # comparison is the relative RMS of the whole energy trace.  Leaving any
+    # one rounding point out of the statement moves it at least 2.5 times
+    # further from the oracle than the faithful statement is: every point is
+    # pinned.
+    from tests.autograd_ref import ROUND_POINTS, mixed_relax_f64
+    sizes = [96, 130, 64, 16]
+    W, b, P = make_net(sizes, seed=5, init="fanin", bias_scale=0.1)
+    x = make_inputs(40, 96, seed=1)
+    top, _, en = oracle.batched_relax(sizes, act, 0.05, W, b, P, x, 15, round_mode=mode, want_energy=True)
+    ttop, ten = mixed_relax_f64(sizes, act, 0.05, W, b, P, x, 15, mode)
+    same = _rel_rms(en, ten)
+    assert same < (1e-5 if mode == "bf16" else 5e-6), same
+    assert close(top, ttop, 2e-3)
+    for point in ROUND_POINTS:
+        _, den = mixed_relax_f64(sizes, act, 0.05, W, b, P, x, 15, mode, drop=(point,))
+        dropped = _rel_rms(en, den)
+        assert dropped > 2.5 * same, (point, dropped, same)
+
+
 def test_rows_are_independent(oracle):
     sizes = [10, 7, 5]
     W, b, P = make_net(sizes, seed=13)
