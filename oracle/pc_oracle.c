@@ -527,6 +527,60 @@ int pco_classify(const int* sizes, int levels, int act, float eta, float act_reg
 }
 
 /*
+ * Adaptive minimum-energy classification, Network.PredictAdaptive
+ * (Network.cs:803-840) with SettleCandidate (:851-867) and SettleAdaptive
+ * (:876-907): every class candidate c of sample b settles from zero hidden
+ * states with the top clamped to one-hot(c), for at most max_steps steps,
+ * leaving after a step once prev - E < epsilon * max(prev, 1e-12) (never after
+ * the first step; epsilon <= 0 never leaves).  F(b, c) is the energy of the
+ * candidate's last step; the class is the first c with the smallest F
+ * (strictly smaller than float.MaxValue to win, :822); the winner is settled
+ * again (:826-828), which repeats its candidate settling exactly, so its
+ * steps count twice and its energy is F(b, c*).  Outputs (each nullable):
+ *   class_energies [batch x C], class_steps [batch x C], best_class [batch],
+ *   best_energy [batch], steps_used [batch] = sum_c steps(b, c) + steps(b, c*).
+ */
+int pco_classify_adaptive(const int* sizes, int levels, int act, float eta, float act_reg, int ffg,
+                          const float* W_all, const float* b_all, const float* prec, int round_mode,
+                          const float* x0, int batch, int max_steps, float epsilon,
+                          float* class_energies, int* class_steps, int* best_class, float* best_energy,
+                          int* steps_used) {
+    if (levels < 2 || batch < 1 || max_steps < 1) return -1;
+    model_t md;
+    setup_model(&md, sizes, levels, act, eta, act_reg, ffg, W_all, b_all, prec, round_mode);
+    md.clamp_top = 1;
+    const int C = sizes[levels - 1], s0 = sizes[0];
+    float** m = calloc((size_t)levels, sizeof(float*));
+    for (int l = 0; l < levels; l++) m[l] = calloc((size_t)sizes[l], sizeof(float));
+    float* fc = malloc(sizeof(float) * (size_t)C);
+    int* sc = malloc(sizeof(int) * (size_t)C);
+    for (int b = 0; b < batch; b++) {
+        float best = 3.402823466e38f;   /* float.MaxValue, :814 */
+        int bc = 0, total = 0;
+        for (int c = 0; c < C; c++) {
+            for (int l = 1; l < levels; l++) memset(m[l], 0, sizeof(float) * sizes[l]);
+            memcpy(m[0], x0 + (size_t)b * s0, sizeof(float) * s0);
+            m[levels - 1][c] = 1.f;
+            float fe = 0.f;
+            sc[c] = relax_batch(&md, m, 1, max_steps, EXIT_RELATIVE, epsilon, NULL, &fe, NULL);
+            fc[c] = fe;
+            total += sc[c];
+            if (class_energies) class_energies[(size_t)b * C + c] = fe;
+            if (class_steps) class_steps[(size_t)b * C + c] = sc[c];
+            if (fe < best) { best = fe; bc = c; }
+        }
+        if (best_class) best_class[b] = bc;
+        if (best_energy) best_energy[b] = fc[bc];
+        if (steps_used) steps_used[b] = total + sc[bc];
+    }
+    free(fc);
+    free(sc);
+    for (int l = 0; l < levels; l++) free(m[l]);
+    free(m);
+    return 0;
+}
+
+/*
  * Learning step, Network.Learn (Network.cs:139-155): settle with input and
  * label clamped, then for every layer l = 1..L-1 Layer.UpdateWeights
  * (Layer.cs:320-333) with the last step's delta_l = f'(pre_l) . e_{l-1}

@@ -69,6 +69,11 @@ def lib():
             _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
             _f32p, _f32p, _f32p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int, _f32p, _i32p, _f32p]
         L.pco_classify.restype = ctypes.c_int
+        L.pco_classify_adaptive.argtypes = [
+            _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+            _f32p, _f32p, _f32p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+            _f32p, _i32p, _i32p, _f32p, _i32p]
+        L.pco_classify_adaptive.restype = ctypes.c_int
         L.pco_learn.argtypes = [
             _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
             _f32p, _f32p, _f32p, ctypes.c_int, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
@@ -253,6 +258,32 @@ def classify(sizes, act, eta, weights, biases, precisions, x0, steps, act_reg=0.
     if rc != 0:
         raise ValueError("oracle rejected arguments")
     return ce, bc, be
+
+
+def classify_adaptive(sizes, act, eta, weights, biases, precisions, x0, max_steps, epsilon, act_reg=0.0,
+                      ffg=False, round_mode="none"):
+    """Network.PredictAdaptive per sample: returns (class_energies [B, C],
+    class_steps [B, C], best_class [B], best_energy [B], steps_used [B])."""
+    sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+    x0 = np.ascontiguousarray(x0, dtype=np.float32)
+    B, C = x0.shape[0], int(sizes[-1])
+    ce = np.empty((B, C), dtype=np.float32)
+    cs = np.empty((B, C), dtype=np.int32)
+    bc = np.empty(B, dtype=np.int32)
+    be = np.empty(B, dtype=np.float32)
+    su = np.empty(B, dtype=np.int32)
+    rc = lib().pco_classify_adaptive(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg),
+                                     _flat(weights, np.float32), _flat(biases, np.float32),
+                                     np.ascontiguousarray(precisions, dtype=np.float32), ROUND[round_mode],
+                                     x0.ravel(), B, int(max_steps), float(epsilon), ce.ravel(), cs.ravel(), bc, be,
+                                     su)
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    return ce, cs, bc, be, su
+
+
+# EffortPresets.For (Networks/EffortLevel.cs:33-39): (maxSteps, epsilon) per effort level
+EFFORT_PRESETS = {"low": (10, 1e-3), "medium": (30, 1e-4), "high": (100, 1e-5)}
 
 
 def learn(sizes, act, eta, weights, biases, precisions, x0, labels, steps, eta_w, weight_decay=0.0,

@@ -192,3 +192,92 @@ def test_mixed_learn_tracks_float_learn(oracle, mode):
         assert close(mw[l], fw[l], 2e-2) and close(mb[l], fb[l], 2e-2)
         assert not np.array_equal(mw[l], fw[l])      # the rounding is really applied
     assert close(me, fe, 5e-2)
+
+
+# ---------------------------------------------------- adaptive classification
+
+def _exit_step_by_hand(trace, max_steps, eps):
+    """SettleAdaptive's rule read off a fixed-step energy trace
+    (Network.cs:895-905): the first step k >= 2 whose energy fell by less than
+    eps * max(previous, 1e-12), in float arithmetic; max_steps if none."""
+    if eps <= 0:
+        return max_steps
+    for k in range(1, max_steps):
+        prev, cur = np.float32(trace[k - 1]), np.float32(trace[k])
+        if prev - cur < np.float32(eps) * max(prev, np.float32(1e-12)):
+            return k + 1
+    return max_steps
+
+
+@pytest.mark.parametrize("act,ffg", [("tanh", False), ("gelu", True), ("sigmoid", False)])
+def test_classify_adaptive_exit_steps_by_hand(oracle, act, ffg):
+    # Each candidate's steps and energy, recomputed from its own fixed-step
+    # clamped settling (one-hot label, pco_clamped_relax) and the exit rule
+    # applied by hand; the winner is the first minimum and its settling counts
+    # twice (Network.cs:803-840).
+    sizes = [12, 20, 9, 4]
+    W, b, P = make_net(sizes, seed=51, bias_scale=0.2)
+    x = make_inputs(5, 12, seed=52, dist="uniform01")
+    T, C = 40, 4
+    for eps in (3e-2, 1e-2, 1e-3):
+        ce, cs, bc, be, su = oracle.classify_adaptive(sizes, act, 0.1, W, b, P, x, T, eps, ffg=ffg)
+        fired = 0
+        for i in range(len(x)):
+            for c in range(C):
+                _, tr = oracle.clamped_relax(sizes, act, 0.1, W, b, P, x[i:i + 1], one_hot([c], C), T, ffg=ffg)
+                k = _exit_step_by_hand(tr[:, 0], T, eps)
+                assert cs[i, c] == k, (eps, i, c, cs[i, c], k)
+                assert ce[i, c] == pytest.approx(float(tr[k - 1, 0]), rel=1e-6)
+                fired += k < T
+            assert bc[i] == int(np.argmin(ce[i]))
+            assert be[i] == ce[i, bc[i]]
+            assert su[i] == cs[i].sum() + cs[i, bc[i]]
+        assert fired > 0, eps
+
+
+def test_classify_adaptive_epsilon_zero_is_predict_with_energy(oracle):
+    # AdaptiveInferenceTests.cs:74-95: epsilon = 0 is PredictWithEnergy exactly,
+    # with every candidate and the winner's re-run at the full budget
+    sizes = [4, 8, 2]
+    W, b, P = make_net(sizes, seed=42)
+    W, b, a, bb = _train_two_patterns(oracle, sizes, 0.1, 0.01, 40, 30, W, b, P)
+    x = np.concatenate([a, bb])
+    ce, bc, be = oracle.classify(sizes, "tanh", 0.1, W, b, P, x, 15)
+    ace, acs, abc, abe, asu = oracle.classify_adaptive(sizes, "tanh", 0.1, W, b, P, x, 15, 0.0)
+    assert np.array_equal(ce, ace) and np.array_equal(bc, abc) and np.array_equal(be, abe)
+    assert np.all(acs == 15) and np.all(asu == 15 * (2 + 1))
+
+
+def test_classify_adaptive_saves_steps_and_stays_correct(oracle):
+    # AdaptiveInferenceTests.cs:116-131: a generous budget (200) and epsilon
+    # 1e-3 after TrainTwoPatterns: pattern a is class 0, finite non-negative
+    # energy, fewer than 200 * (2 + 1) steps spent.
+    sizes = [4, 8, 2]
+    W, b, P = make_net(sizes, seed=42)
+    W, b, a, bb = _train_two_patterns(oracle, sizes, 0.1, 0.01, 40, 30, W, b, P)
+    _, cs, bc, be, su = oracle.classify_adaptive(sizes, "tanh", 0.1, W, b, P, np.concatenate([a, bb]), 200, 1e-3)
+    assert list(bc) == [0, 1]
+    assert np.all(np.isfinite(be)) and np.all(be >= 0)
+    assert np.all(su < 200 * 3), su
+
+
+def test_classify_adaptive_monotone_in_epsilon_and_budget_invariant(oracle):
+    # AdaptiveInferenceTests.cs:97-114 applied per candidate: a looser epsilon
+    # stops no later, and an exit inside the budget does not move when the
+    # budget grows
+    sizes = [10, 16, 6, 3]
+    W, b, P = make_net(sizes, seed=61, bias_scale=0.1)
+    x = make_inputs(6, 10, seed=62, dist="uniform01")
+    _, loose, _, _, _ = oracle.classify_adaptive(sizes, "tanh", 0.1, W, b, P, x, 60, 1e-2)
+    _, tight, _, _, _ = oracle.classify_adaptive(sizes, "tanh", 0.1, W, b, P, x, 60, 1e-4)
+    _, wide, _, _, _ = oracle.classify_adaptive(sizes, "tanh", 0.1, W, b, P, x, 200, 1e-2)
+    assert np.all(loose <= tight) and np.any(loose < 60)
+    assert np.array_equal(loose[loose < 60], wide[loose < 60])
+
+
+def test_effort_presets(oracle):
+    # EffortPresets.For (EffortLevel.cs:33-39) and AdaptiveInferenceTests.cs:133-142:
+    # steps grow and the tolerance tightens with the effort level
+    low, med, high = (oracle.EFFORT_PRESETS[k] for k in ("low", "medium", "high"))
+    assert (low, med, high) == ((10, 1e-3), (30, 1e-4), (100, 1e-5))
+    assert low[0] < med[0] < high[0] and low[1] > med[1] > high[1]
