@@ -187,6 +187,22 @@ int pcd_pc_model_destroy(pcd_model* model);
 int pcd_pc_relax(pcd_model* model, const float* x0, int batch, int steps,
                  float* out_top, float* out_states, float* out_energy, void* stream);
 
+/* No counterpart in the reference: pcd_pc_relax for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * pcd_pc_relax, but the call allocates nothing: its scratch (states, deltas,
+ * energy partials, split-K partial tiles) lives in a library-owned device
+ * array of 64 MiB per device, which each device holds until the process ends,
+ * and the step loop runs as plain kernel launches (no cached graph).  A call
+ * whose batch needs more scratch than that fails with PCD_INVALID_VALUE
+ * before launching anything (pcd_last_error names the size).  Every call on a
+ * device shares that device's array, so calls that overlap on one device
+ * (other streams, other threads, other models) race and must be serialised by
+ * the caller.  out_energy, when given, is written in place.  Asynchronous on
+ * `stream`. */
+int pcd_pc_relax_noalloc(pcd_model* model, const float* x0, int batch, int steps,
+                         float* out_top, float* out_states, float* out_energy, void* stream);
+
 /* Ragged request batches: request r owns rows [row_offsets[r], row_offsets[r+1])
  * of x0_packed and settles for at most steps[r] steps, leaving early by
  * exit_rule / exit_threshold (enum pcd_exit_rule) -- Network.InferAdaptive

@@ -51,6 +51,7 @@ _SIGNATURES = {
     "pcd_pc_model_create": [P_int, c_int, c_int, c_float, c_float, c_int, P_void_p, P_void_p, P_float, c_int, P_void_p],
     "pcd_pc_model_destroy": [c_void_p],
     "pcd_pc_relax": [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p],
+    "pcd_pc_relax_noalloc": [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p],
     "pcd_pc_relax_ragged": [c_void_p, c_void_p, P_int, P_int, c_int, c_int, c_float, P_int, c_void_p, P_float, c_void_p],
     "pcd_pc_relax_clamped": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p],
     "pcd_pc_classify": [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p],

@@ -1378,6 +1378,127 @@ int pcd_pc_relax(pcd_model* m, const float* x0, int batch, int steps, float* out
     return PCD_SUCCESS;
 }
 
+}  // extern "C"
+
+// ------------------------------------------------- allocation-free relaxation
+
+// Scratch of pcd_pc_relax_noalloc: every buffer its settling needs besides the
+// caller's inputs and outputs (states, their 16-bit copies, deltas, folded
+// updates, energy partials, split-K partial tiles and counters), carved per
+// call.  Each device the library runs on holds its own copy of the array
+// until the process ends.  In host code the name is a host-side stand-in, not
+// a device address: host code uses only the address scratch_base() looks up.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_base[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on `device`, which must be current: looked
+// up with hipGetSymbolAddress on the first call for that device, then kept
+// (each device holds the array at its own address).
+int scratch_base(int device, char** out) {
+    if (device < 0 || device >= kMaxScratchDevices)
+        return fail(PCD_INVALID_VALUE, "device %d beyond the %d the scratch table covers", device, kMaxScratchDevices);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_base[device]) {
+        void* p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(PCD_HIP_ERROR, "hipGetSymbolAddress(scratch) gave a null address");
+        g_scratch_base[device] = (char*)p;
+    }
+    *out = g_scratch_base[device];
+    return PCD_SUCCESS;
+}
+
+// Lays out the workspace of a `batch`-row settling with `tile` from `base`:
+// the buffers ensure_workspace allocates (energy slots for this tile only),
+// then split-K scratch for exactly the partial tiles this call's phases use
+// (the split plan itself is the allocating path's, so the kernels and their
+// results are the same).  Returns the bytes the layout spans.
+size_t carve_workspace(const pcd_model* m, char* base, int batch, Tile tile, Workspace& w) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        char* p = base + off;
+        off += round_up(bytes, 256);
+        return p;
+    };
+    const int L = m->L, ob = op_bytes(m->dtype);
+    w.cap = (int)round_up((size_t)batch, kRowPad);
+    const size_t cap = (size_t)w.cap;
+    w.M.assign(L, nullptr);
+    w.S.assign(L, nullptr);
+    w.D.assign(L, nullptr);
+    w.E.assign(L, nullptr);
+    for (int l = 0; l < L; ++l) {
+        w.M[l] = (float*)take(cap * m->P[l] * 4);
+        if (l >= 1 && m->dtype != PCD_F32) w.S[l] = take(cap * m->P[l] * ob);
+        if (l >= 1) w.D[l] = take(cap * m->P[l - 1] * ob);
+        if (l >= 1 && l <= L - 2) w.E[l] = (float*)take(cap * m->P[l] * 4);
+    }
+    w.slots_cap = energy_slots(m, tile);
+    w.energy_part = (float*)take((size_t)w.slots_cap * cap * 4);
+    w.split_count = (int*)take((size_t)split_part_tiles(m) * 4);
+    w.split_part = (float*)(base + off);
+    std::vector<ProblemSet> err, upd;
+    int nslots = 0;
+    build_phase_sets(m, &w, batch, tile, 0, err, upd, &nslots);
+    size_t end = off;
+    for (const auto* sets : {&err, &upd})
+        for (const ProblemSet& ps : *sets)
+            for (int i = 0; i < ps.n; ++i)
+                if (ps.p[i].ksplit > 1)
+                    end = std::max(end, (size_t)((const char*)(ps.p[i].part + (size_t)ps.p[i].tiles * tile.m * tile.n) -
+                                                 base));
+    return round_up(end, 256);
+}
+
+}  // namespace
+
+extern "C" {
+
+int pcd_pc_relax_noalloc(pcd_model* m, const float* x0, int batch, int steps, float* out_top, float* out_states,
+                         float* out_energy, void* stream_) {
+    if (int st = check_model(m)) return st;
+    if (batch < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
+    if (steps < 1) return fail(PCD_INVALID_VALUE, "inferenceSteps must be >= 1, got %d", steps);
+    if (!x0 || !out_top) return fail(PCD_INVALID_VALUE, "pcd_pc_relax_noalloc: null pointer");
+    hipStream_t s = (hipStream_t)stream_;
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    char* base = nullptr;
+    if (int st = scratch_base(m->device, &base)) return st;
+    const Tile tile = choose_tile(m, batch);
+    Workspace w;
+    w.stream = s;
+    const size_t need = carve_workspace(m, base, batch, tile, w);
+    if (need > kNoAllocScratchBytes)
+        return fail(PCD_INVALID_VALUE,
+                    "pcd_pc_relax_noalloc: %d rows of this model need %zu bytes of scratch, beyond its %zu; use "
+                    "pcd_pc_relax", batch, need, kNoAllocScratchBytes);
+    // The array keeps whatever the last call on this device left in it: clear
+    // the whole span (the K padding of the states and deltas and the split-K
+    // counters must read zero) with a kernel, which also records into a
+    // captured graph.
+    if (int st = launch_zero(base, need, s)) return st;
+    const int L = m->L;
+    HIP_TRY(hipMemcpy2DAsync(w.M[0], (size_t)m->P[0] * 4, x0, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, batch,
+                             hipMemcpyDeviceToDevice, s));
+    RelaxSpec r;
+    r.batch = batch;
+    r.steps = steps;
+    r.tile = tile;
+    r.energy_out = out_energy;   // [steps x batch], written in place
+    if (int st = enqueue_relax(m, &w, r, s, nullptr)) return st;
+    if (int st = copy_out_rows(out_top, m->s[L - 1], w.M[L - 1], m->P[L - 1], batch, s)) return st;
+    if (out_states)
+        if (int st = copy_out_states(m, &w, out_states, batch, s)) return st;
+    return PCD_SUCCESS;
+}
+
 int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_offsets, const int* steps, int requests,
                         int exit_rule, float exit_threshold, int* steps_used, float* out_top, float* out_energy,
                         void* stream_) {
