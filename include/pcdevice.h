@@ -248,6 +248,32 @@ int pcd_pc_relax_clamped(pcd_model* model, const float* x0, const float* top, in
 int pcd_pc_classify(pcd_model* model, const float* x0, int batch, int steps, float* out_class_energies,
                     int* out_class, float* out_energy, void* stream);
 
+/* Adaptive minimum-energy classification of a batch: Network.PredictAdaptive
+ * (Network.cs:803-840) for every sample at once.  Each class candidate c of
+ * sample b (row b * C + c, C = sizes[levels-1]) settles from zero hidden
+ * states with the top clamped to one-hot(c), as SettleCandidate (:851-867),
+ * for at most max_steps steps, and stops after a step once
+ * prev - E < epsilon * max(prev, 1e-12) (SettleAdaptive, :876-907; never after
+ * the first step; epsilon <= 0 never stops, which is pcd_pc_classify).  E(b, c)
+ * is the candidate's energy at its last step; the class is the first c with
+ * the smallest E; the reference re-runs the winner (:826-828), which repeats
+ * its candidate's settling: its energy is E(b, c*) and its steps count twice.
+ * EffortPresets.For (EffortLevel.cs:33-39) gives (max_steps, epsilon):
+ * Low (10, 1e-3), Medium (30, 1e-4), High (100, 1e-5).  Device pointers, each
+ * nullable but not all null:
+ *   x0                  [batch x sizes[0]]
+ *   out_class_energies  [batch x C]   E(b, c)
+ *   out_class_steps     [batch x C]   steps candidate c of sample b ran
+ *   out_class           [batch]       the class (PredictAdaptive's cls)
+ *   out_energy          [batch]       its energy (energy)
+ *   out_steps_used      [batch]       sum over c of the steps, plus the
+ *                                     winner's again (stepsUsed)
+ * Errors: PCD_INVALID_VALUE for batch < 1 ("Empty batch."), max_steps < 1,
+ * a null input or no output.  Asynchronous on `stream`. */
+int pcd_pc_classify_adaptive(pcd_model* model, const float* x0, int batch, int max_steps, float epsilon,
+                             float* out_class_energies, int* out_class_steps, int* out_class, float* out_energy,
+                             int* out_steps_used, void* stream);
+
 /* Learning step, Network.Learn (Network.cs:139-155): settles with x0 and
  * `labels` clamped (as pcd_pc_relax_clamped), then updates every layer's
  * weights in place with Layer.UpdateWeights (Layer.cs:320-333), the last step's

@@ -7,6 +7,7 @@ all computing through the hand-written gfx950 kernels in csrc/.
 """
 from .batched_pc_forward import BatchedPcForward, PcDeviceModel
 from .device import Device, DeviceKind, DeviceRuntime, DeviceTensor, Event, Stream, TensorOps
+from .effort import EffortLevel, EffortPresets
 from .errors import (ArgumentException, ArgumentNullException, ArgumentOutOfRangeException, DeviceException,
                      DeviceStatus, NotSupportedException)
 from .gemm import Gemm, HipGemmProvider, IGemmProvider
@@ -15,6 +16,6 @@ from .snapshot import ActivationType, GenerativeSnapshot
 __all__ = [
     "ActivationType", "ArgumentException", "ArgumentNullException", "ArgumentOutOfRangeException",
     "BatchedPcForward", "Device", "DeviceException", "DeviceKind", "DeviceRuntime", "DeviceStatus",
-    "DeviceTensor", "Event", "Gemm", "GenerativeSnapshot", "HipGemmProvider", "IGemmProvider",
+    "DeviceTensor", "EffortLevel", "EffortPresets", "Event", "Gemm", "GenerativeSnapshot", "HipGemmProvider", "IGemmProvider",
     "NotSupportedException", "PcDeviceModel", "Stream", "TensorOps",
 ]

@@ -21,6 +21,7 @@ import numpy as np
 from . import _native
 from ._native import DTYPE, EXIT, MEMCPY, call
 from .device import DeviceTensor, Stream
+from .effort import EffortLevel, EffortPresets
 from .errors import ArgumentException, ArgumentNullException, ArgumentOutOfRangeException
 from .snapshot import GenerativeSnapshot
 
@@ -236,6 +237,42 @@ class PcDeviceModel:
             for t in (dx, ce, cls, be):
                 t.free()
         return out
+
+    def classify_adaptive_device(self, x0_ptr: int, batch: int, max_steps: int, epsilon: float,
+                                 class_energies_ptr: int | None = None, class_steps_ptr: int | None = None,
+                                 class_ptr: int | None = None, energy_ptr: int | None = None,
+                                 steps_used_ptr: int | None = None, stream: Stream | None = None) -> None:
+        """pcd_pc_classify_adaptive on device pointers, queued on `stream` (no sync)."""
+        call("pcd_pc_classify_adaptive", self.handle, x0_ptr, int(batch), int(max_steps), float(epsilon),
+             class_energies_ptr, class_steps_ptr, class_ptr, energy_ptr, steps_used_ptr,
+             stream.handle if stream else None)
+
+    def classify_adaptive(self, x0: np.ndarray, max_steps: int, epsilon: float, stream: Stream | None = None):
+        """Network.PredictAdaptive (Network.cs:803-840) for every sample of a host
+        batch.  Returns (class_energies [B x C], class_steps [B x C], class [B],
+        energy [B], steps_used [B])."""
+        x0 = self._batch_in(x0, self.sizes[0], "inputs")
+        if max_steps < 1:
+            raise ArgumentOutOfRangeException("maxSteps")
+        B, C = x0.shape[0], self.sizes[-1]
+        dx = DeviceTensor.from_host(x0)
+        outs = [DeviceTensor((B, C)), DeviceTensor((B, C), dtype=np.int32), DeviceTensor((B,), dtype=np.int32),
+                DeviceTensor((B,)), DeviceTensor((B,), dtype=np.int32)]
+        try:
+            self.classify_adaptive_device(dx.ptr, B, max_steps, epsilon, *[t.ptr for t in outs], stream=stream)
+            self._sync(stream)
+            res = tuple(t.to_host() for t in outs)
+        finally:
+            for t in [dx, *outs]:
+                t.free()
+        return res
+
+    def predict_adaptive(self, x0: np.ndarray, effort: EffortLevel, stream: Stream | None = None):
+        """PredictAdaptive with a named effort preset (Network.cs:843-847):
+        returns (class [B], energy [B], steps_used [B])."""
+        max_steps, epsilon = EffortPresets.for_level(effort)
+        _, _, cls, energy, used = self.classify_adaptive(x0, max_steps, epsilon, stream)
+        return cls, energy, used
 
     def learn_device(self, x0_ptr: int, labels_ptr: int, batch: int, steps: int, eta_w: float,
                      weight_decay: float = 0.0, energy_ptr: int | None = None, stream: Stream | None = None) -> None:

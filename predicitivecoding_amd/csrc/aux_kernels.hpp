@@ -106,6 +106,69 @@ __global__ void exit_kernel(const float* __restrict__ part, int ldp, int nslots,
     }
 }
 
+// exit_kernel for calls whose every request is one row (request r is row r):
+// one thread per request.  The same sum and the same decision as exit_kernel
+// (whose tree over one row's value only adds zeros).
+__global__ void exit_rows_kernel(const float* __restrict__ part, int ldp, int nslots, int requests,
+                                 int* __restrict__ done_at, float* __restrict__ prev_energy,
+                                 float* __restrict__ last_energy, int t, int rule, float thr) {
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < requests; r += gridDim.x * blockDim.x) {
+        if (t >= done_at[r]) continue;
+        const float e = sum_slots(part, ldp, nslots, r);
+        const float prev = prev_energy[r];
+        bool stop = false;
+        if (rule == 1) stop = thr > 0.f && t > 0 && (prev - e < thr * fmaxf(prev, 1e-12f));
+        else if (rule == 2) stop = e < thr;
+        last_energy[r] = e;
+        prev_energy[r] = e;
+        if (stop) done_at[r] = t + 1;
+    }
+}
+
+// Tables of a call whose every request is one row (request r is row r):
+// row -> request, row offsets, step budgets, exit state.
+__global__ void row_request_tables_kernel(int* __restrict__ row_req, int* __restrict__ offsets,
+                                          int* __restrict__ done_at, float* __restrict__ prev_energy,
+                                          float* __restrict__ last_energy, int rows, int steps) {
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= rows; r += gridDim.x * blockDim.x) {
+        offsets[r] = r;
+        if (r < rows) {
+            row_req[r] = r;
+            done_at[r] = steps;
+            prev_energy[r] = 0.f;
+            last_energy[r] = 0.f;
+        }
+    }
+}
+
+// Adaptive classification (Network.PredictAdaptive, Network.cs:803-840): row
+// b * classes + c settled candidate c of sample b for done_at steps and ended
+// at energy e.  The class is the first c with the smallest energy (below
+// float.MaxValue, :822); the winner's re-run (:826-828) repeats its settling,
+// so its energy is its candidate's and its steps count twice.  Each output is
+// written where its pointer is set.
+__global__ void adaptive_argmin_kernel(const float* __restrict__ e, const int* __restrict__ done_at, int batch,
+                                       int classes, float* __restrict__ table, int* __restrict__ steps_table,
+                                       int* __restrict__ cls, float* __restrict__ best, int* __restrict__ steps_used) {
+    for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < batch; b += gridDim.x * blockDim.x) {
+        float be = 3.402823466e38f;   // float.MaxValue
+        int bc = 0, total = 0;
+        for (int c = 0; c < classes; ++c) {
+            const size_t r = (size_t)b * classes + c;
+            const float v = e[r];
+            const int k = done_at[r];
+            if (table) table[r] = v;
+            if (steps_table) steps_table[r] = k;
+            total += k;
+            if (v < be) { be = v; bc = c; }
+        }
+        const size_t w = (size_t)b * classes + bc;
+        if (cls) cls[b] = bc;
+        if (best) best[b] = e[w];
+        if (steps_used) steps_used[b] = total + done_at[w];
+    }
+}
+
 // Ragged: the row tiles of bm rows that hold a row still running at step t
 // (a row of request r runs while t < done_at[r]), listed in increasing order,
 // and their number.  One workgroup of kActTilesThreads threads; at most

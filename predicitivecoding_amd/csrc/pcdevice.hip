@@ -722,7 +722,14 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
         for (auto& ps : err)
             if ((st = launch_phase(m->dtype, tile, EPI_ERROR, ps, a, s))) return st;
         if (timer) HIP_TRY(hipEventRecord(e1, s));
-        if (r.row_req) {
+        if (r.row_req && r.requests == batch) {
+            // every request is one row (offsets increase strictly): a thread per request
+            const int grid = std::min((batch + 255) / 256, 1024);
+            hipLaunchKernelGGL(exit_rows_kernel, dim3(grid), dim3(256), 0, s, (const float*)w->energy_part, w->cap,
+                               nslots, r.requests, r.done_at, r.prev_energy, r.last_energy, t, r.exit_rule,
+                               r.exit_thr);
+            if ((st = from_hip(hipGetLastError(), "exit_rows_kernel launch"))) return st;
+        } else if (r.row_req) {
             hipLaunchKernelGGL(exit_kernel, dim3(r.requests), dim3(256), 0, s, (const float*)w->energy_part, w->cap,
                                nslots, r.row_offsets, r.done_at, r.prev_energy, r.last_energy, t, r.exit_rule,
                                r.exit_thr);
@@ -1747,22 +1754,103 @@ int pcd_pc_classify(pcd_model* m, const float* x0, int batch, int steps, float* 
     }
     if (int st = stage_top(m, w, nullptr, rows, s)) return st;
     // Eager runs write the energies into a stream-ordered scratch buffer.
-    void* scratch = nullptr;
+    void* energy_buf = nullptr;
     if (m->profile || !m->use_graph)
-        if (int st = pool_alloc(&scratch, (size_t)steps * rows * 4, s)) return st;
+        if (int st = pool_alloc(&energy_buf, (size_t)steps * rows * 4, s)) return st;
     const float* energy = nullptr;
-    int st = run_relax(m, w, rows, steps, 1, 1, (float*)scratch, s, &energy);
+    int st = run_relax(m, w, rows, steps, 1, 1, (float*)energy_buf, s, &energy);
     if (!st) {
         const int grid = std::min((batch + 255) / 256, 1024);
         hipLaunchKernelGGL(class_argmin_kernel, dim3(grid), dim3(256), 0, s, energy + (size_t)(steps - 1) * rows,
                            batch, C, out_class_energies, out_class, out_energy);
         st = from_hip(hipGetLastError(), "class_argmin_kernel launch");
     }
-    if (scratch) {
-        int st2 = pool_free(scratch, s);
+    if (energy_buf) {
+        int st2 = pool_free(energy_buf, s);
         if (!st) st = st2;
     }
     return st;
+}
+
+int pcd_pc_classify_adaptive(pcd_model* m, const float* x0, int batch, int max_steps, float epsilon,
+                             float* out_class_energies, int* out_class_steps, int* out_class, float* out_energy,
+                             int* out_steps_used, void* stream_) {
+    if (int st = check_model(m)) return st;
+    if (batch < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
+    if (max_steps < 1) return fail(PCD_INVALID_VALUE, "maxSteps must be >= 1, got %d", max_steps);
+    if (!x0) return fail(PCD_INVALID_VALUE, "pcd_pc_classify_adaptive: null input");
+    if (!out_class_energies && !out_class_steps && !out_class && !out_energy && !out_steps_used)
+        return fail(PCD_INVALID_VALUE, "pcd_pc_classify_adaptive: no output requested");
+    const int C = m->s[m->L - 1];
+    const long rows_l = (long)batch * C;
+    if (rows_l > (1L << 30))
+        return fail(PCD_INVALID_VALUE, "pcd_pc_classify_adaptive: %d x %d rows is too many", batch, C);
+    const int rows = (int)rows_l;
+    hipStream_t s = (hipStream_t)stream_;
+    std::lock_guard<std::mutex> g(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    Workspace* w = nullptr;
+    if (int st = ensure_workspace(m, s, rows, &w)) return st;
+    // Candidate c of sample b is row b * C + c (SettleCandidate, Network.cs:851-867):
+    // layer 0 its sample, the top one-hot(c), the hidden layers from zero.
+    {
+        const size_t n = (size_t)rows * m->s[0];
+        const int grid = (int)std::min<size_t>((n + 255) / 256, 8192);
+        hipLaunchKernelGGL(replicate_rows_kernel, dim3(grid), dim3(256), 0, s, x0, m->s[0], C, rows, w->M[0],
+                           m->P[0]);
+        if (int st = from_hip(hipGetLastError(), "replicate_rows_kernel launch")) return st;
+    }
+    if (int st = stage_top(m, w, nullptr, rows, s)) return st;
+    // Every candidate is a request of one row that leaves by the relative rule
+    // (SettleAdaptive, :876-907).  The tables take the ragged layout in the
+    // workspace buffer (offsets fixed by rows and requests, which a cached
+    // graph relies on), written on the device.
+    if (!w->rg_tables) {
+        const size_t cap_bytes = (size_t)w->cap * 4 + (size_t)(w->cap + 1) * 4 + (size_t)w->cap * 4 * 3 +
+                                 (size_t)w->cap * 4;
+        if (int st = dev_alloc_zero(w->owned, &w->rg_tables, cap_bytes)) return st;
+    }
+    int* d_row_req = (int*)w->rg_tables;
+    int* d_offsets = d_row_req + rows;
+    int* d_done = d_offsets + rows + 1;
+    float* d_prev = (float*)(d_done + rows);
+    float* d_last = d_prev + rows;
+    {
+        const int grid = std::min((rows + 256) / 256, 4096);
+        hipLaunchKernelGGL(row_request_tables_kernel, dim3(grid), dim3(256), 0, s, d_row_req, d_offsets, d_done,
+                           d_prev, d_last, rows, max_steps);
+        if (int st = from_hip(hipGetLastError(), "row_request_tables_kernel launch")) return st;
+    }
+    RelaxSpec r;
+    r.batch = rows;
+    r.steps = max_steps;
+    r.tile = choose_tile(m, rows);
+    r.clamp_top = 1;
+    r.row_req = d_row_req;
+    r.done_at = d_done;
+    r.row_offsets = d_offsets;
+    r.requests = rows;
+    r.exit_rule = PCD_EXIT_RELATIVE;
+    r.exit_thr = epsilon;
+    r.prev_energy = d_prev;
+    r.last_energy = d_last;
+    int st = PCD_SUCCESS;
+    if (m->profile || !m->use_graph) {
+        PhaseTimer timer;
+        st = enqueue_relax(m, w, r, s, m->profile ? &timer : nullptr);
+        if (m->profile) {
+            int st2 = collect_timer(m, timer, s);
+            if (!st) st = st2;
+        }
+    } else {
+        Plan* p = get_plan(m, w, r, 0, &st);
+        if (p) st = from_hip(hipGraphLaunch(p->exec, s), "hipGraphLaunch");
+    }
+    if (st) return st;
+    const int grid = std::min((batch + 255) / 256, 1024);
+    hipLaunchKernelGGL(adaptive_argmin_kernel, dim3(grid), dim3(256), 0, s, (const float*)d_last, (const int*)d_done,
+                       batch, C, out_class_energies, out_class_steps, out_class, out_energy, out_steps_used);
+    return from_hip(hipGetLastError(), "adaptive_argmin_kernel launch");
 }
 
 int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, int steps, float eta_w,
@@ -1780,12 +1868,12 @@ int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, 
     HIP_TRY(hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, batch,
                              hipMemcpyDeviceToDevice, s));
     if (int st = stage_top(m, w, labels, batch, s)) return st;
-    void* scratch = nullptr;
+    void* energy_buf = nullptr;
     const bool want_energy = out_energy != nullptr;
     if (want_energy && (m->profile || !m->use_graph))
-        if (int st = pool_alloc(&scratch, (size_t)steps * batch * 4, s)) return st;
+        if (int st = pool_alloc(&energy_buf, (size_t)steps * batch * 4, s)) return st;
     const float* energy = nullptr;
-    int st = run_relax(m, w, batch, steps, 1, want_energy, (float*)scratch, s, &energy);
+    int st = run_relax(m, w, batch, steps, 1, want_energy, (float*)energy_buf, s, &energy);
     if (!st && want_energy) {
         hipError_t e = hipMemcpyAsync(out_energy, energy + (size_t)(steps - 1) * batch, (size_t)batch * 4,
                                       hipMemcpyDeviceToDevice, s);
@@ -1869,8 +1957,8 @@ int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, 
         int st2 = pool_free(t, s);
         if (!st) st = st2;
     }
-    if (scratch) {
-        int st2 = pool_free(scratch, s);
+    if (energy_buf) {
+        int st2 = pool_free(energy_buf, s);
         if (!st) st = st2;
     }
     return st;
