@@ -280,7 +280,11 @@ int pcd_pc_classify_adaptive(pcd_model* model, const float* x0, int batch, int m
  * delta_l = f'(pre_l) * e_{l-1} and the settled states:
  *   W_l += eta_w delta_l^T mu_l,  b_l += eta_w sum delta_l,  W_l -= eta_w weight_decay W_l.
  * A batch applies the sum of its samples' updates, all taken at the weights
- * the call starts from (batch = 1 is exactly Learn).  Device pointers:
+ * the call starts from.  The hidden layers start from zero: with batch = 1
+ * this is Learn on a network whose hidden states are zero (fresh, or after a
+ * resetState settling).  The reference's Learn starts from the hidden states
+ * the network last persisted (ReadAllLayers, :143) and persists the settled
+ * ones; pcd_pc_learn_warm takes and returns them.  Device pointers:
  *   x0 [batch x sizes[0]], labels [batch x sizes[levels-1]],
  *   out_energy nullable [batch], each sample's energy at the last step.
  * A 16-bit model keeps fp32 master weights and updates those, then re-rounds
@@ -291,6 +295,21 @@ int pcd_pc_classify_adaptive(pcd_model* model, const float* x0, int batch, int m
  * Asynchronous on `stream`. */
 int pcd_pc_learn(pcd_model* model, const float* x0, const float* labels, int batch, int steps, float eta_w,
                  float weight_decay, float* out_energy, void* stream);
+
+/* pcd_pc_learn with the hidden states carried as Network.Learn carries them
+ * (Network.cs:139-155: ReadAllLayers restores each layer's persisted Mu,
+ * InferCore resets nothing, _store.Write persists the settled Mu).  Device
+ * pointers, the hidden layers l = 1..levels-2 as [batch x sizes[l]] blocks
+ * concatenated in layer order:
+ *   hidden_in   nullable; the states the settling starts from (null: zero)
+ *   hidden_out  nullable; the settled states, to pass as the next call's
+ *               hidden_in (may alias hidden_in)
+ * With the same model, passing each call's hidden_out to the next reproduces
+ * the reference's sequence of Learn calls on one network.  Otherwise as
+ * pcd_pc_learn.  Asynchronous on `stream`. */
+int pcd_pc_learn_warm(pcd_model* model, const float* x0, const float* labels, const float* hidden_in,
+                      float* hidden_out, int batch, int steps, float eta_w, float weight_decay, float* out_energy,
+                      void* stream);
 
 /* Reads layer `layer`'s (1..levels-1) current weights back to host memory, as
  * Network.ExportGenerativeSnapshot copies them (Network.cs:1328-1356):

@@ -598,7 +598,8 @@ int pco_classify_adaptive(const int* sizes, int levels, int act, float eta, floa
 int pco_learn(const int* sizes, int levels, int act, float eta, float act_reg, int ffg,
               float* W_all, float* b_all, const float* prec, int round_mode,
               const float* x0, const float* labels, int batch, int steps,
-              float eta_w, float weight_decay, float* out_energy) {
+              float eta_w, float weight_decay, float* out_energy,
+              const float* hidden_in, float* hidden_out) {
     if (levels < 2 || batch < 1 || steps < 1) return -1;
     model_t md;
     setup_model(&md, sizes, levels, act, eta, act_reg, ffg, W_all, b_all, prec, round_mode);
@@ -610,8 +611,25 @@ int pco_learn(const int* sizes, int levels, int act, float eta, float act_reg, i
     for (int l = 1; l < L; l++) d[l] = calloc((size_t)batch * sizes[l - 1], sizeof(float));
     memcpy(m[0], x0, sizeof(float) * (size_t)batch * sizes[0]);
     memcpy(m[L - 1], labels, sizeof(float) * (size_t)batch * sizes[L - 1]);
+    /* Learn settles from the hidden states the network holds (ReadAllLayers,
+     * Network.cs:143, restores each layer's persisted Mu; InferCore resets
+     * nothing); hidden_in carries them, null is a network at zero.  The
+     * settled hidden states go to hidden_out, the Mu that _store.Write
+     * persists for the next call (:150-151). */
+    size_t hoff = 0;
+    if (hidden_in)
+        for (int l = 1; l <= L - 2; l++) {
+            memcpy(m[l], hidden_in + hoff, sizeof(float) * (size_t)batch * sizes[l]);
+            hoff += (size_t)batch * sizes[l];
+        }
     float* trace = calloc((size_t)steps * batch, sizeof(float));
     relax_batch(&md, m, batch, steps, EXIT_NONE, 0.f, trace, NULL, d);
+    hoff = 0;
+    if (hidden_out)
+        for (int l = 1; l <= L - 2; l++) {
+            memcpy(hidden_out + hoff, m[l], sizeof(float) * (size_t)batch * sizes[l]);
+            hoff += (size_t)batch * sizes[l];
+        }
     if (out_energy) memcpy(out_energy, trace + (size_t)(steps - 1) * batch, sizeof(float) * batch);
     free(trace);
     for (int l = 1; l < L; l++) {

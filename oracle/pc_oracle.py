@@ -77,7 +77,7 @@ def lib():
         L.pco_learn.argtypes = [
             _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
             _f32p, _f32p, _f32p, ctypes.c_int, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
-            ctypes.c_float, _vp]
+            ctypes.c_float, _vp, _vp, _vp]
         L.pco_learn.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -287,10 +287,13 @@ EFFORT_PRESETS = {"low": (10, 1e-3), "medium": (30, 1e-4), "high": (100, 1e-5)}
 
 
 def learn(sizes, act, eta, weights, biases, precisions, x0, labels, steps, eta_w, weight_decay=0.0,
-          act_reg=0.0, ffg=False, round_mode="none"):
+          act_reg=0.0, ffg=False, round_mode="none", hidden=None, want_hidden=False):
     """Network.Learn on a batch (B = 1 is the reference call; B > 1 sums the
     per-sample updates at the pre-call weights); with a 16-bit round_mode,
-    LearnMixed on fp32 masters.  Returns (new weights, new biases, energy [B])."""
+    LearnMixed on fp32 masters.  `hidden` (a list of [B x s_l] arrays for
+    l = 1..L-2, or None for zeros) is the hidden state the settling starts
+    from, as the network persisted it.  Returns (new weights, new biases,
+    energy [B]), plus the settled hidden states with want_hidden."""
     sizes = np.ascontiguousarray(sizes, dtype=np.int32)
     x0 = np.ascontiguousarray(x0, dtype=np.float32)
     B = x0.shape[0]
@@ -298,10 +301,16 @@ def learn(sizes, act, eta, weights, biases, precisions, x0, labels, steps, eta_w
     W = _flat(weights, np.float32).copy()
     b = _flat(biases, np.float32).copy()
     energy = np.empty(B, dtype=np.float32)
+    nh = B * int(sizes[1:-1].sum())
+    h_in = None if hidden is None else np.concatenate([np.ascontiguousarray(h, np.float32).ravel() for h in hidden])
+    if h_in is not None and h_in.size != nh:
+        raise ValueError("hidden must hold the hidden layers' [B x s_l] states")
+    h_out = np.empty(max(nh, 1), dtype=np.float32)
     rc = lib().pco_learn(sizes, len(sizes), ACT[act], eta, act_reg, int(ffg), W, b,
                          np.ascontiguousarray(precisions, dtype=np.float32), ROUND[round_mode], x0.ravel(),
                          labels.ravel(),
-                         B, int(steps), float(eta_w), float(weight_decay), _ptr(energy))
+                         B, int(steps), float(eta_w), float(weight_decay), _ptr(energy),
+                         _ptr(h_in) if h_in is not None and nh else None, _ptr(h_out))
     if rc != 0:
         raise ValueError("oracle rejected arguments")
     new_w, new_b, wo, bo = [], [], 0, 0
@@ -311,4 +320,10 @@ def learn(sizes, act, eta, weights, biases, precisions, x0, labels, steps, eta_w
         new_b.append(b[bo:bo + lo])
         wo += lo * sz
         bo += lo
-    return new_w, new_b, energy
+    if not want_hidden:
+        return new_w, new_b, energy
+    out, off = [], 0
+    for l in range(1, len(sizes) - 1):
+        out.append(h_out[off:off + B * int(sizes[l])].reshape(B, int(sizes[l])))
+        off += B * int(sizes[l])
+    return new_w, new_b, energy, out

@@ -58,6 +58,8 @@ _SIGNATURES = {
     "pcd_pc_classify_adaptive": [c_void_p, c_void_p, c_int, c_int, c_float, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p],
     "pcd_pc_learn": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_float, c_void_p, c_void_p],
+    "pcd_pc_learn_warm": [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_float, c_void_p,
+                          c_void_p],
     "pcd_pc_model_get_weights": [c_void_p, c_int, c_void_p, c_void_p],
     "pcd_pc_model_load_record": [c_void_p, c_int, c_void_p, c_size_t],
     "pcd_pc_model_info": [c_void_p, P_int, P_int, c_int, P_int],

@@ -281,24 +281,48 @@ class PcDeviceModel:
              float(weight_decay), energy_ptr, stream.handle if stream else None)
 
     def learn(self, x0: np.ndarray, labels: np.ndarray, steps: int, eta_w: float, weight_decay: float = 0.0,
-              stream: Stream | None = None) -> np.ndarray:
+              stream: Stream | None = None, hidden=None, want_hidden: bool = False):
         """Network.Learn on a host batch (the sum of the per-sample updates);
-        returns each sample's energy at the last step."""
+        returns each sample's energy at the last step.  `hidden` (a list of
+        [B x s_l] arrays for l = 1..L-2, or None for zeros) is the hidden state
+        the settling starts from, as the reference's network holds it between
+        calls (pcd_pc_learn_warm); with want_hidden the settled hidden states
+        come back too, as (energy, hidden)."""
         x0 = self._batch_in(x0, self.sizes[0], "inputs")
         B = x0.shape[0]
         labels = np.ascontiguousarray(labels, dtype=np.float32).reshape(B, self.sizes[-1])
         if steps < 1:
             raise ArgumentOutOfRangeException("inferenceSteps")
+        hs = self.sizes[1:-1]
+        if hidden is not None:
+            hidden = [np.ascontiguousarray(h, dtype=np.float32).reshape(B, s) for h, s in zip(hidden, hs)]
+            if len(hidden) != len(hs):
+                raise ArgumentException(f"hidden must hold {len(hs)} layers")
         dx, dl = DeviceTensor.from_host(x0), DeviceTensor.from_host(labels)
         en = DeviceTensor((B,))
+        nh = B * sum(hs)
+        dh_in = DeviceTensor.from_host(np.concatenate([h.ravel() for h in hidden])) if hidden and nh else None
+        dh_out = DeviceTensor((nh,)) if want_hidden and nh else None
         try:
-            self.learn_device(dx.ptr, dl.ptr, B, steps, eta_w, weight_decay, en.ptr, stream)
+            if dh_in is None and dh_out is None:
+                self.learn_device(dx.ptr, dl.ptr, B, steps, eta_w, weight_decay, en.ptr, stream)
+            else:
+                call("pcd_pc_learn_warm", self.handle, dx.ptr, dl.ptr, dh_in.ptr if dh_in else None,
+                     dh_out.ptr if dh_out else None, B, int(steps), float(eta_w), float(weight_decay), en.ptr,
+                     stream.handle if stream else None)
             self._sync(stream)
             energy = en.to_host()
+            out = []
+            if want_hidden:
+                flat, off = dh_out.to_host() if dh_out else np.zeros(0, np.float32), 0
+                for s in hs:
+                    out.append(flat[off:off + B * s].reshape(B, s))
+                    off += B * s
         finally:
-            for t in (dx, dl, en):
-                t.free()
-        return energy
+            for t in (dx, dl, en, dh_in, dh_out):
+                if t is not None:
+                    t.free()
+        return (energy, out) if want_hidden else energy
 
     def load_record(self, layer: int, record: bytes) -> None:
         """pcd_pc_model_load_record: one LayerSerializer record (the layer's

@@ -268,7 +268,7 @@ struct Workspace {
 };
 
 struct Plan {
-    int batch = 0, steps = 0, want_energy = 0, clamp_top = 0;
+    int batch = 0, steps = 0, want_energy = 0, clamp_top = 0, keep_hidden = 0;
     Tile tile{0, 0};
     // ragged loops (requests > 0): their tables live in the workspace at
     // offsets fixed by (batch, requests), so these complete the key
@@ -606,6 +606,7 @@ struct RelaxSpec {
     int batch = 0, steps = 0;
     Tile tile{0, 0};
     int clamp_top = 0;              // layer L-1 holds rows staged by the caller and is never updated
+    int keep_hidden = 0;            // layers 1..L-2 start from rows staged by the caller, not from zero
     float* energy_out = nullptr;    // [steps x batch] per-row energies (nullable)
     // ragged early exit (row_req null: fixed steps for every row)
     const int* row_req = nullptr;
@@ -655,6 +656,7 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
     int st;
     for (int l = 1; l < L; ++l) {
         if (l == L - 1 && r.clamp_top) break;
+        if (l <= L - 2 && r.keep_hidden) continue;
         if ((st = launch_zero(w->M[l], (size_t)w->cap * m->P[l] * 4, s))) return st;
         if (w->S[l] && (st = launch_zero(w->S[l], (size_t)w->cap * m->P[l] * op_bytes(m->dtype), s))) return st;
     }
@@ -766,7 +768,8 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
     const int requests = r.row_req ? r.requests : 0;
     for (auto& p : w->plans)
         if (p->batch == r.batch && p->steps == r.steps && p->want_energy == want_energy &&
-            p->clamp_top == r.clamp_top && p->tile.m == r.tile.m && p->tile.n == r.tile.n &&
+            p->clamp_top == r.clamp_top && p->keep_hidden == r.keep_hidden && p->tile.m == r.tile.m &&
+            p->tile.n == r.tile.n &&
             p->requests == requests && (requests == 0 || (p->exit_rule == r.exit_rule &&
                                                           std::memcmp(&p->exit_thr, &r.exit_thr, 4) == 0))) {
             p->last_use = ++m->clock;
@@ -787,6 +790,7 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
     p->steps = r.steps;
     p->want_energy = want_energy;
     p->clamp_top = r.clamp_top;
+    p->keep_hidden = r.keep_hidden;
     p->tile = r.tile;
     p->requests = requests;
     p->exit_rule = requests ? r.exit_rule : 0;
@@ -819,12 +823,13 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
 // [steps x batch] row energies when want_energy is set (the caller's
 // `caller_energy` or the plan's own), valid once the stream reaches it.
 int run_relax(pcd_model* m, Workspace* w, int batch, int steps, int clamp_top, int want_energy, float* caller_energy,
-              hipStream_t s, const float** energy) {
+              hipStream_t s, const float** energy, int keep_hidden = 0) {
     RelaxSpec r;
     r.batch = batch;
     r.steps = steps;
     r.tile = choose_tile(m, batch);
     r.clamp_top = clamp_top;
+    r.keep_hidden = keep_hidden;
     *energy = nullptr;
     if (m->profile || !m->use_graph) {
         float* buf = caller_energy;
@@ -1652,10 +1657,10 @@ int pcd_pc_relax_ragged(pcd_model* m, const float* x0_packed, const int* row_off
 
 // ------------------------------------------- clamped settling, classes, learning
 
-// Writes the clamped top rows of a settling: src [rows x s_top] packed, or,
-// with src null, the one-hot label of class r % s_top for row r.
-static int stage_top(pcd_model* m, Workspace* w, const float* src, int rows, hipStream_t s) {
-    const int lt = m->L - 1;
+// Writes rows of layer lt's state (and its operand-type copy) before a
+// settling: src [rows x s_lt] packed, or, with src null, the one-hot label of
+// class r % s_lt for row r.  Columns past s_lt are written zero.
+static int stage_rows(pcd_model* m, Workspace* w, int lt, const float* src, int rows, hipStream_t s) {
     const size_t n = (size_t)rows * m->P[lt];
     const int grid = (int)std::min<size_t>((n + 255) / 256, 8192);
     switch (m->dtype) {
@@ -1673,6 +1678,11 @@ static int stage_top(pcd_model* m, Workspace* w, const float* src, int rows, hip
         break;
     }
     return from_hip(hipGetLastError(), "top_rows_kernel launch");
+}
+
+// The clamped top rows of a settling (see stage_rows).
+static int stage_top(pcd_model* m, Workspace* w, const float* src, int rows, hipStream_t s) {
+    return stage_rows(m, w, m->L - 1, src, rows, s);
 }
 
 // After the fp32 weights of layer l changed (the fp32 W itself, or a 16-bit
@@ -1853,13 +1863,17 @@ int pcd_pc_classify_adaptive(pcd_model* m, const float* x0, int batch, int max_s
     return from_hip(hipGetLastError(), "adaptive_argmin_kernel launch");
 }
 
-int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, int steps, float eta_w,
-                 float weight_decay, float* out_energy, void* stream_) {
+}  // extern "C"
+
+// The learning step (pcd_pc_learn, pcd_pc_learn_warm): settle from hidden_in
+// (null: zero hidden states), hand the settled hidden states to hidden_out
+// (nullable), then update every layer's weights.
+static int learn_step(pcd_model* m, const float* x0, const float* labels, const float* hidden_in, float* hidden_out,
+                      int batch, int steps, float eta_w, float weight_decay, float* out_energy, hipStream_t s) {
     if (int st = check_model(m)) return st;
     if (batch < 1) return fail(PCD_INVALID_VALUE, "Empty batch.");
     if (steps < 1) return fail(PCD_INVALID_VALUE, "inferenceSteps must be >= 1, got %d", steps);
     if (!x0 || !labels) return fail(PCD_INVALID_VALUE, "pcd_pc_learn: null pointer");
-    hipStream_t s = (hipStream_t)stream_;
     std::lock_guard<std::mutex> g(m->mu);
     HIP_TRY(hipSetDevice(m->device));
     Workspace* w = nullptr;
@@ -1868,16 +1882,31 @@ int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, 
     HIP_TRY(hipMemcpy2DAsync(w->M[0], (size_t)m->P[0] * 4, x0, (size_t)m->s[0] * 4, (size_t)m->s[0] * 4, batch,
                              hipMemcpyDeviceToDevice, s));
     if (int st = stage_top(m, w, labels, batch, s)) return st;
+    const bool warm = hidden_in != nullptr && L > 2;
+    if (warm) {
+        size_t off = 0;
+        for (int l = 1; l <= L - 2; ++l) {
+            if (int st = stage_rows(m, w, l, hidden_in + off, batch, s)) return st;
+            off += (size_t)batch * m->s[l];
+        }
+    }
     void* energy_buf = nullptr;
     const bool want_energy = out_energy != nullptr;
     if (want_energy && (m->profile || !m->use_graph))
         if (int st = pool_alloc(&energy_buf, (size_t)steps * batch * 4, s)) return st;
     const float* energy = nullptr;
-    int st = run_relax(m, w, batch, steps, 1, want_energy, (float*)energy_buf, s, &energy);
+    int st = run_relax(m, w, batch, steps, 1, want_energy, (float*)energy_buf, s, &energy, warm ? 1 : 0);
     if (!st && want_energy) {
         hipError_t e = hipMemcpyAsync(out_energy, energy + (size_t)(steps - 1) * batch, (size_t)batch * 4,
                                       hipMemcpyDeviceToDevice, s);
         st = from_hip(e, "learn energy copy");
+    }
+    if (!st && hidden_out) {
+        size_t off = 0;
+        for (int l = 1; l <= L - 2 && !st; ++l) {
+            st = copy_out_rows(hidden_out + off, m->s[l], w->M[l], m->P[l], batch, s);
+            off += (size_t)batch * m->s[l];
+        }
     }
 
     // Hebbian step of every layer (Layer.UpdateWeights, Layer.cs:320-333):
@@ -1962,6 +1991,20 @@ int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, 
         if (!st) st = st2;
     }
     return st;
+}
+
+extern "C" {
+
+int pcd_pc_learn(pcd_model* m, const float* x0, const float* labels, int batch, int steps, float eta_w,
+                 float weight_decay, float* out_energy, void* stream) {
+    return learn_step(m, x0, labels, nullptr, nullptr, batch, steps, eta_w, weight_decay, out_energy,
+                      (hipStream_t)stream);
+}
+
+int pcd_pc_learn_warm(pcd_model* m, const float* x0, const float* labels, const float* hidden_in, float* hidden_out,
+                      int batch, int steps, float eta_w, float weight_decay, float* out_energy, void* stream) {
+    return learn_step(m, x0, labels, hidden_in, hidden_out, batch, steps, eta_w, weight_decay, out_energy,
+                      (hipStream_t)stream);
 }
 
 int pcd_pc_model_get_weights(pcd_model* m, int layer, float* W_out, float* b_out) {

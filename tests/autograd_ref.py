@@ -27,11 +27,12 @@ def _act(name):
 
 
 def autograd_relax(sizes, act, eta, W, b, prec, x0, steps, act_reg=0.0, ffg=False, top_clamp=None,
-                   want_delta=False):
-    """Settles from zero hidden states; with top_clamp [B, s_top] the top layer
-    is held there (not a free variable).  With want_delta it also returns, for
-    every layer l >= 1, delta_l = -dF/dpre_l at the last step's pre-update
-    state (autograd through the pre-activation itself)."""
+                   want_delta=False, init_hidden=None):
+    """Settles from zero hidden states (or from init_hidden, a list of [B, s_l]
+    arrays for l = 1..L-2); with top_clamp [B, s_top] the top layer is held
+    there (not a free variable).  With want_delta it also returns, for every
+    layer l >= 1, delta_l = -dF/dpre_l at the last step's pre-update state
+    (autograd through the pre-activation itself)."""
     f = _act(act)
     L = len(sizes)
     dt = torch.float64
@@ -41,6 +42,9 @@ def autograd_relax(sizes, act, eta, W, b, prec, x0, steps, act_reg=0.0, ffg=Fals
     x = torch.tensor(np.asarray(x0, dtype=np.float64), dtype=dt)
     B = x.shape[0]
     mu = [x] + [torch.zeros(B, s, dtype=dt) for s in sizes[1:]]
+    if init_hidden is not None:
+        for l, h in enumerate(init_hidden, start=1):
+            mu[l] = torch.tensor(np.asarray(h, dtype=np.float64), dtype=dt).reshape(B, sizes[l])
     nfree = L - 1
     if top_clamp is not None:
         mu[-1] = torch.tensor(np.asarray(top_clamp, dtype=np.float64), dtype=dt).reshape(B, sizes[-1])
@@ -83,11 +87,14 @@ def autograd_relax(sizes, act, eta, W, b, prec, x0, steps, act_reg=0.0, ffg=Fals
     return mu[-1].numpy(), [m.numpy() for m in mu], energies
 
 
-def autograd_learn(sizes, act, eta, W, b, prec, x0, labels, steps, eta_w, weight_decay=0.0):
+def autograd_learn(sizes, act, eta, W, b, prec, x0, labels, steps, eta_w, weight_decay=0.0, init_hidden=None,
+                   want_hidden=False):
     """Learning step from the autograd settling: W_l += eta_w delta_l^T mu_l
-    (settled mu_l), b_l += eta_w sum delta_l, then W_l -= eta_w lambda W_l."""
+    (settled mu_l), b_l += eta_w sum delta_l, then W_l -= eta_w lambda W_l.
+    The settling starts from init_hidden (zeros if None); with want_hidden the
+    settled hidden states come back too."""
     _, mus, energies, deltas = autograd_relax(sizes, act, eta, W, b, prec, x0, steps, top_clamp=labels,
-                                              want_delta=True)
+                                              want_delta=True, init_hidden=init_hidden)
     new_w, new_b = [], []
     for l in range(1, len(sizes)):
         w = np.asarray(W[l - 1], dtype=np.float64) + eta_w * deltas[l].T @ mus[l]
@@ -96,6 +103,8 @@ def autograd_learn(sizes, act, eta, W, b, prec, x0, labels, steps, eta_w, weight
             w = w - eta_w * weight_decay * w
         new_w.append(w)
         new_b.append(bb)
+    if want_hidden:
+        return new_w, new_b, energies[-1], mus[1:-1]
     return new_w, new_b, energies[-1]
 
 

@@ -250,3 +250,57 @@ def test_learn_mixed_predicts_like_float(oracle):
         m.close()
     assert list(cls) == [0, 1]
     assert all(np.all(np.isfinite(w)) for w in gw)
+
+
+@pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("bf16", 2e-3)])
+def test_learn_from_hidden_states(oracle, dtype, tol):
+    # pcd_pc_learn_warm: the settling starts from given hidden states (the Mu a
+    # reference network holds between Learn calls) and returns the settled ones
+    sizes = [37, 70, 19, 6]
+    snap, W, b, P, x = build_case(sizes, "tanh", 0.1, batch=7, bias_scale=0.1, seed=19)
+    y = _one_hot(np.arange(7) % 6, 6)
+    rng = np.random.default_rng(20)
+    hidden = [(rng.standard_normal((7, s)) * 0.4).astype(np.float32) for s in sizes[1:-1]]
+    m = _model(snap, dtype)
+    try:
+        en, gh = m.learn(x, y, 9, 0.05, hidden=hidden, want_hidden=True)
+        gw, gb = m.get_weights()
+    finally:
+        m.close()
+    rw, rb, ren, rh = oracle.learn(sizes, "tanh", 0.1, W, b, P, x, y, 9, 0.05, round_mode=ROUND[dtype],
+                                   hidden=hidden, want_hidden=True)
+    errs = dict(weights=max(max_rel(a, r) for a, r in zip(gw, rw)), biases=max(max_rel(a, r) for a, r in zip(gb, rb)),
+                energy=max_rel(en, ren), hidden=max(max_rel(a, r) for a, r in zip(gh, rh)))
+    _report(f"learn warm {dtype}", **errs)
+    assert all(v < tol for v in errs.values()), errs
+
+
+def test_train_two_patterns_with_carried_hidden_state(oracle):
+    # TrainTwoPatterns as the reference runs it on one network: each Learn
+    # starts from the hidden state the previous one settled to (Network.cs:143,
+    # 150-151).  Device chain against the oracle chain, call after call.
+    sizes = [4, 8, 2]
+    W, b, P = make_net(sizes, seed=42)
+    from predicitivecoding_amd import GenerativeSnapshot
+    snap = GenerativeSnapshot(sizes, ACT["tanh"], 0.1, 0.0, False, W, b, list(P))
+    a = np.array([[1, 0, 0, 0]], np.float32)
+    bb = np.array([[0, 0, 0, 1]], np.float32)
+    m = _model(snap)
+    rw, rb, rh = W, b, None
+    gh = None
+    worst = 0.0
+    try:
+        for _ in range(40):
+            for x, y in ((a, _one_hot([0], 2)), (bb, _one_hot([1], 2))):
+                _, gh = m.learn(x, y, 30, 0.01, hidden=gh, want_hidden=True)
+                rw, rb, _, rh = oracle.learn(sizes, "tanh", 0.1, rw, rb, P, x, y, 30, 0.01, hidden=rh,
+                                             want_hidden=True)
+                worst = max(worst, max_rel(gh[0], rh[0]))
+        gw, gb = m.get_weights()
+        _, cls, _ = m.classify(np.concatenate([a, bb]), 15)
+    finally:
+        m.close()
+    werr = max(max_rel(g, r) for g, r in zip(gw + gb, rw + rb))
+    _report("two patterns, carried hidden state", weights=werr, hidden=worst)
+    assert werr < 1e-4 and worst < 1e-4
+    assert list(cls) == [0, 1]

@@ -281,3 +281,59 @@ def test_effort_presets(oracle):
     low, med, high = (oracle.EFFORT_PRESETS[k] for k in ("low", "medium", "high"))
     assert (low, med, high) == ((10, 1e-3), (30, 1e-4), (100, 1e-5))
     assert low[0] < med[0] < high[0] and low[1] > med[1] > high[1]
+
+
+# ------------------------------------------ learning from carried hidden states
+
+@pytest.mark.parametrize("act", ["tanh", "gelu"])
+def test_learn_from_hidden_states_matches_autograd(oracle, act):
+    # Network.Learn settles from the hidden states the network holds
+    # (ReadAllLayers, Network.cs:143; InferCore resets nothing), and persists
+    # the settled ones (:150-151).  The oracle's warm-started step against the
+    # float64 autograd statement started from the same states: weights, biases,
+    # energies and the settled hidden states.
+    sizes = [10, 14, 9, 3]
+    W, b, P = make_net(sizes, seed=31, bias_scale=0.2)
+    x = make_inputs(4, 10, seed=32, dist="uniform01")
+    y = one_hot([0, 2, 1, 2], 3)
+    rng = np.random.default_rng(33)
+    hidden = [(rng.standard_normal((4, s)) * 0.5).astype(np.float32) for s in sizes[1:-1]]
+    nw, nb, en, nh = oracle.learn(sizes, act, 0.1, W, b, P, x, y, 12, 0.05, hidden=hidden, want_hidden=True)
+    rw, rb, ren, rh = autograd_learn(sizes, act, 0.1, W, b, P, x, y, 12, 0.05, init_hidden=hidden, want_hidden=True)
+    for l in range(len(nw)):
+        assert close(nw[l], rw[l], 1e-5) and close(nb[l], rb[l], 1e-5)
+    assert close(en, ren, 1e-5)
+    for a, c in zip(nh, rh):
+        assert close(a, c, 1e-5)
+    # the start matters: from zero the step is another one
+    zw, _, _ = oracle.learn(sizes, act, 0.1, W, b, P, x, y, 12, 0.05)
+    assert not close(zw[0], nw[0], 1e-3)
+    # no hidden states given is a network at zero, bit for bit
+    z2, _, _ = oracle.learn(sizes, act, 0.1, W, b, P, x, y, 12, 0.05,
+                            hidden=[np.zeros((4, s), np.float32) for s in sizes[1:-1]])
+    assert all(np.array_equal(a, c) for a, c in zip(zw, z2))
+
+
+def test_train_two_patterns_with_carried_hidden_state(oracle):
+    # AdaptiveInferenceTests.TrainTwoPatterns as the reference runs it: Learn(a,
+    # 0), Learn(b, 1), ... on one network, each call starting from the hidden
+    # state the previous one settled to.  The oracle's chain with the state
+    # carried equals the autograd chain with the state carried, call after
+    # call; and it is not the chain that restarts every call from zero.
+    sizes = [4, 8, 2]
+    W, b, P = make_net(sizes, seed=42)
+    a = np.array([[1, 0, 0, 0]], np.float32)
+    bb = np.array([[0, 0, 0, 1]], np.float32)
+    ow, ob, oh = W, b, [np.zeros((1, 8), np.float32)]
+    rw, rb, rh = [w.astype(np.float64) for w in W], [v.astype(np.float64) for v in b], [np.zeros((1, 8))]
+    zw, zb = W, b
+    for _ in range(6):
+        for x, y in ((a, one_hot([0], 2)), (bb, one_hot([1], 2))):
+            ow, ob, _, oh = oracle.learn(sizes, "tanh", 0.1, ow, ob, P, x, y, 30, 0.01, hidden=oh, want_hidden=True)
+            rw, rb, _, rh = autograd_learn(sizes, "tanh", 0.1, rw, rb, P, x, y, 30, 0.01, init_hidden=rh,
+                                           want_hidden=True)
+            zw, zb, _ = oracle.learn(sizes, "tanh", 0.1, zw, zb, P, x, y, 30, 0.01)
+            for l in range(2):
+                assert close(ow[l], rw[l], 1e-5) and close(ob[l], rb[l], 1e-5)
+            assert close(oh[0], rh[0], 1e-5)
+    assert not close(ow[0], zw[0], 1e-4)
