@@ -152,6 +152,18 @@ int pcd_gemm_bf16(const uint16_t* dA, const uint16_t* dB, float* dC, int m, int 
 /* fp16 operands: CudaGemmProvider.MatMulMixedDevice (CudaGemmProvider.cs:185-202). */
 int pcd_gemm_f16(const uint16_t* dA, const uint16_t* dB, float* dC, int m, int k, int n,
                  int trans_a, int trans_b, float beta, void* stream);
+/* Strided batched GEMM, CudaGemmProvider.MatMulBatchedDevice
+ * (CudaGemmProvider.cs:130-141): for i < batch, row-major
+ * C_i[m,n] = A_i[m,k] B_i[k,n] with A_i at dA + i*m*k, B_i at dB + i*k*n and
+ * C_i at dC + i*m*n (elements); fp32 C.  The _bf16 and _f16 forms take 16-bit
+ * operands (raw bit patterns) with fp32 accumulation.  Scratch for operand
+ * packing comes from the library's pool. */
+int pcd_gemm_f32_batched(const float* dA, const float* dB, float* dC, int batch, int m, int k, int n,
+                         void* stream);
+int pcd_gemm_bf16_batched(const uint16_t* dA, const uint16_t* dB, float* dC, int batch, int m, int k, int n,
+                          void* stream);
+int pcd_gemm_f16_batched(const uint16_t* dA, const uint16_t* dB, float* dC, int batch, int m, int k, int n,
+                         void* stream);
 
 /* --------------------------------------------------------- PC relaxation */
 

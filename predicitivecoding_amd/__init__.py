@@ -11,11 +11,12 @@ from .effort import EffortLevel, EffortPresets
 from .errors import (ArgumentException, ArgumentNullException, ArgumentOutOfRangeException, DeviceException,
                      DeviceStatus, NotSupportedException)
 from .gemm import Gemm, HipGemmProvider, IGemmProvider
+from .registry import DeviceRegistry
 from .snapshot import ActivationType, GenerativeSnapshot
 
 __all__ = [
     "ActivationType", "ArgumentException", "ArgumentNullException", "ArgumentOutOfRangeException",
-    "BatchedPcForward", "Device", "DeviceException", "DeviceKind", "DeviceRuntime", "DeviceStatus",
+    "BatchedPcForward", "Device", "DeviceException", "DeviceRegistry", "DeviceKind", "DeviceRuntime", "DeviceStatus",
     "DeviceTensor", "EffortLevel", "EffortPresets", "Event", "Gemm", "GenerativeSnapshot", "HipGemmProvider", "IGemmProvider",
     "NotSupportedException", "PcDeviceModel", "Stream", "TensorOps",
 ]

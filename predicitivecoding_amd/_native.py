@@ -48,6 +48,9 @@ _SIGNATURES = {
     "pcd_gemm_f32": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p],
     "pcd_gemm_bf16": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p],
     "pcd_gemm_f16": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p],
+    "pcd_gemm_f32_batched": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p],
+    "pcd_gemm_bf16_batched": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p],
+    "pcd_gemm_f16_batched": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p],
     "pcd_pc_model_create": [P_int, c_int, c_int, c_float, c_float, c_int, P_void_p, P_void_p, P_float, c_int, P_void_p],
     "pcd_pc_model_destroy": [c_void_p],
     "pcd_pc_relax": [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p],

@@ -43,6 +43,28 @@ __global__ void pack_kernel(const void* __restrict__ src, int src_is_f32, int ro
     }
 }
 
+// pack_kernel over `batch` matrices stored back to back: item i of src is the
+// [rows x cols] matrix (or [cols x rows] read transposed) at src + i * rows *
+// cols, packed into the zero-padded [prow x pcol] buffer at dst + i * prow *
+// pcol (row pitch pcol).
+template <typename OP>
+__global__ void pack_batched_kernel(const void* __restrict__ src, int src_is_f32, int batch, int rows, int cols,
+                                    int trans, void* __restrict__ dst, int prow, int pcol) {
+    const size_t per = (size_t)prow * pcol, n = per * batch, src_per = (size_t)rows * cols;
+    for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < n; k += (size_t)gridDim.x * blockDim.x) {
+        const size_t item = k / per, e = k % per;
+        const int r = (int)(e / pcol), c = (int)(e % pcol);
+        const bool inside = r < rows && c < cols;
+        const size_t s = item * src_per + (trans ? (size_t)c * rows + r : (size_t)r * cols + c);
+        if (src_is_f32) {
+            OpTraits<OP>::store(dst, k, inside ? ((const float*)src)[s] : 0.f);
+        } else {
+            // 16-bit source of the operand's own type: copy the bits
+            ((uint16_t*)dst)[k] = inside ? ((const uint16_t*)src)[s] : (uint16_t)0;
+        }
+    }
+}
+
 // Weight formats of a LayerSerializer record (Model/LayerSerializer.cs:19-36).
 enum RecordKind { REC_F32 = 0, REC_F16 = 1, REC_BF16 = 2, REC_I8 = 3 };
 

@@ -1166,6 +1166,95 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     return st;
 }
 
+// Strided batched GEMM: C_i = A_i B_i for i < batch, row-major, A_i [m x k] at
+// dA + i m k, B_i [k x n] at dB + i k n, C_i [m x n] at dC + i m n.  Both
+// operands of every item are packed K-contiguous in one launch each; the
+// items are the problems of grouped phase launches (kMaxProblems per launch),
+// their tiles dealt over the XCDs together.
+static int gemm_batched_common(int dtype, const void* dA, const void* dB, float* dC, int batch, int m, int k, int n,
+                               void* stream_) {
+    if (!dA || !dB || !dC) return fail(PCD_INVALID_VALUE, "pcd_gemm_batched: null pointer");
+    if (batch < 1 || m < 1 || k < 1 || n < 1)
+        return fail(PCD_INVALID_VALUE, "pcd_gemm_batched: bad shape %d x (%d x %d x %d)", batch, m, k, n);
+    hipStream_t s = (hipStream_t)stream_;
+    int dev = 0, cus = 256;
+    HIP_TRY(hipGetDevice(&dev));
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    auto tiles = [&](int t) { return (long)batch * ((m + t - 1) / t) * ((n + t - 1) / t); };
+    const Tile tile = (dtype != PCD_F32 && tiles(256) >= cus) ? Tile{256, 256}
+                      : tiles(128) >= cus                     ? Tile{128, 128}
+                                                              : Tile{64, 64};
+    const int mp = (int)round_up(m, tile.m), np = (int)round_up(n, tile.n), kp = (int)round_up(k, kFeatPad);
+    const int ob = op_bytes(dtype);
+    const size_t a_item = (size_t)mp * kp * ob, b_item = (size_t)np * kp * ob;
+    void *pa = nullptr, *pb = nullptr;
+    int st = pool_alloc(&pa, a_item * batch, s);
+    if (!st) st = pool_alloc(&pb, b_item * batch, s);
+    auto pack = [&](const void* src, int rows, int cols, int trans, void* dst, int prow, int pcol) -> int {
+        const int grid = (int)std::min<size_t>(((size_t)batch * prow * pcol + 255) / 256, 16384);
+        const int f32 = dtype == PCD_F32;
+        switch (dtype) {
+        case PCD_F32: hipLaunchKernelGGL(pack_batched_kernel<float>, dim3(grid), dim3(256), 0, s, src, f32, batch, rows, cols, trans, dst, prow, pcol); break;
+        case PCD_BF16: hipLaunchKernelGGL(pack_batched_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, src, f32, batch, rows, cols, trans, dst, prow, pcol); break;
+        default: hipLaunchKernelGGL(pack_batched_kernel<f16_t>, dim3(grid), dim3(256), 0, s, src, f32, batch, rows, cols, trans, dst, prow, pcol); break;
+        }
+        return from_hip(hipGetLastError(), "pack_batched_kernel launch");
+    };
+    // the kernel's A is A_i [m x k]; its B is B_i^T [n x k] (B_i read transposed)
+    if (!st) st = pack(dA, m, k, 0, pa, mp, kp);
+    if (!st) st = pack(dB, n, k, 1, pb, np, kp);
+    PhaseArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.alpha = 1.f;
+    a.beta = 0.f;
+    a.k_stagger = dtype == PCD_F32 ? 0 : auto_k_stagger(kp / stage_k(dtype, tile));
+    for (int i0 = 0; i0 < batch && !st; i0 += kMaxProblems) {
+        ProblemSet ps;
+        std::memset(&ps, 0, sizeof ps);
+        ps.n = std::min(kMaxProblems, batch - i0);
+        for (int q = 0; q < ps.n; ++q) {
+            const size_t i = (size_t)(i0 + q);
+            Problem& p = ps.p[q];
+            p.A = (const char*)pa + i * a_item;
+            p.lda = kp;
+            p.B = (const char*)pb + i * b_item;
+            p.ldb = kp;
+            p.M = m;
+            p.N = n;
+            p.K = kp;
+            p.tiles_m = mp / tile.m;
+            p.tiles_n = np / tile.n;
+            p.tiles = p.tiles_m * p.tiles_n;
+            p.ldo = n;
+            p.m = dC + i * (size_t)m * n;
+        }
+        st = launch_phase(dtype, tile, EPI_PLAIN, ps, a, s);
+    }
+    if (pa) {
+        int st2 = pool_free(pa, s);
+        if (!st) st = st2;
+    }
+    if (pb) {
+        int st2 = pool_free(pb, s);
+        if (!st) st = st2;
+    }
+    return st;
+}
+
+int pcd_gemm_f32_batched(const float* dA, const float* dB, float* dC, int batch, int m, int k, int n, void* stream) {
+    return gemm_batched_common(PCD_F32, dA, dB, dC, batch, m, k, n, stream);
+}
+
+int pcd_gemm_bf16_batched(const uint16_t* dA, const uint16_t* dB, float* dC, int batch, int m, int k, int n,
+                          void* stream) {
+    return gemm_batched_common(PCD_BF16, dA, dB, dC, batch, m, k, n, stream);
+}
+
+int pcd_gemm_f16_batched(const uint16_t* dA, const uint16_t* dB, float* dC, int batch, int m, int k, int n,
+                         void* stream) {
+    return gemm_batched_common(PCD_F16, dA, dB, dC, batch, m, k, n, stream);
+}
+
 int pcd_gemm_f32(const float* dA, const float* dB, float* dC, int m, int k, int n, int trans_a, int trans_b,
                  float beta, void* stream) {
     return gemm_common(PCD_F32, dA, dB, dC, m, k, n, trans_a, trans_b, beta, stream);

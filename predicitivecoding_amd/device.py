@@ -210,6 +210,30 @@ class TensorOps:
         return out
 
     @staticmethod
+    def mat_mul_batched(a: DeviceTensor, b: DeviceTensor, out: DeviceTensor | None = None,
+                        stream: Stream | None = None) -> DeviceTensor:
+        """Strided batched product of [batch x m x k] and [batch x k x n] tensors
+        into an fp32 [batch x m x n] (MatMulBatchedDevice, CudaGemmProvider.cs:130-141;
+        16-bit operands as in mat_mul)."""
+        if len(a.shape) != 3 or len(b.shape) != 3 or a.shape[0] != b.shape[0]:
+            raise ArgumentException("batched MatMul needs [batch x m x k] and [batch x k x n] tensors")
+        if a.dtype != b.dtype or a.dtype not in _GEMM_FN:
+            raise ArgumentException(f"MatMul operands must share one of float32, float16 or uint16 (bf16); "
+                                    f"got {a.dtype} and {b.dtype}")
+        batch, m, k = a.shape
+        _, k2, n = b.shape
+        if k != k2:
+            raise ArgumentException(f"inner dimensions differ: {k} vs {k2}")
+        if out is None:
+            out = DeviceTensor((batch, m, n), np.float32, stream)
+        elif out.shape != (batch, m, n) or out.dtype != np.float32:
+            raise ArgumentException("out must be an fp32 [batch x m x n] tensor")
+        call(_GEMM_FN[a.dtype] + "_batched", a.ptr, b.ptr, out.ptr, batch, m, k, n, stream.handle if stream else None)
+        if stream is None:
+            call("pcd_device_synchronize")
+        return out
+
+    @staticmethod
     def copy_to(src: DeviceTensor, dst: DeviceTensor, stream: Stream | None = None) -> None:
         if src.nbytes != dst.nbytes:
             raise ArgumentException("size mismatch")

@@ -34,19 +34,38 @@ def _check(a, m, k, b, n):
 
 
 class HipGemmProvider(IGemmProvider):
+    """The GPU provider on one device (CudaGemmProvider(deviceId), CudaGemmProvider.cs:19-28)."""
+
+    def __init__(self, device_id: int = 0):
+        self.device_id = int(device_id)
+
+    def _device(self):
+        call("pcd_set_device", self.device_id)
+
     def mat_mul(self, a, m, k, b, n):
         a, b = _check(a, m, k, b, n)
+        self._device()
         with DeviceTensor.from_host(a) as da, DeviceTensor.from_host(b) as db, DeviceTensor((m, n)) as dc:
             call("pcd_gemm_f32", da.ptr, db.ptr, dc.ptr, m, k, n, 0, 0, 0.0, None)
             return dc.to_host()
 
     def mat_mul_mixed(self, a, m, k, b, n):
         a, b = _check(a, m, k, b, n)
+        self._device()
         ah = a.astype(np.float16).view(np.uint16)
         bh = b.astype(np.float16).view(np.uint16)
         with DeviceTensor.from_host(ah) as da, DeviceTensor.from_host(bh) as db, DeviceTensor((m, n)) as dc:
             call("pcd_gemm_f16", da.ptr, db.ptr, dc.ptr, m, k, n, 0, 0, 0.0, None)
             return dc.to_host()
+
+    def mat_mul_batched_device(self, dA: int, dB: int, dC: int, batch: int, m: int, k: int, n: int,
+                               stream=None) -> None:
+        """MatMulBatchedDevice (CudaGemmProvider.cs:130-141): C_i = A_i B_i for
+        i < batch on device pointers, items m*k, k*n and m*n floats apart;
+        queued on `stream`."""
+        self._device()
+        call("pcd_gemm_f32_batched", dA, dB, dC, int(batch), int(m), int(k), int(n),
+             stream.handle if stream else None)
 
 
 class Gemm:
