@@ -380,7 +380,19 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *                that stop early fill whole row tiles that drop out (default);
  *                0: in the caller's order.  fp32 results are the same.
  *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
- *                time every phase launch with HIP events (pcd_pc_profile_result) */
+ *                time every phase launch with HIP events (pcd_pc_profile_result)
+ *   persistent   1: a fixed-step fp32 settling whose phases deal at most two
+ *                workgroups per CU (64 x 64 tiles, at most 6 problems a phase)
+ *                runs as one cooperative launch of the whole step loop, with
+ *                grid barriers between the phases; the call then waits for
+ *                the settling.  Results are the phase launches' bit for bit.
+ *                Default 0: on MI355X a grid barrier costs about what a graph
+ *                node's launch does, and the graph replay is faster.
+ *   persist_spin polls of a persistent grid barrier before it gives up (the
+ *                call then fails with PCD_HIP_ERROR and every workgroup exits);
+ *                default 4194304
+ *   persist_grid workgroups of the persistent launch, a multiple of 8 (0:
+ *                automatic; capped at what the device holds at once) */
 int pcd_pc_set_option(pcd_model* model, const char* name, int value);
 /* Average duration (ms) of the error-phase and update-phase kernels over the
  * launches of the last profiled call, and their launch counts. */

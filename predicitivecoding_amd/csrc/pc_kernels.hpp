@@ -40,6 +40,7 @@
 //   row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include <type_traits>
@@ -477,17 +478,28 @@ template <typename OP> struct PackOp {
     }
 };
 
+typedef const __attribute__((address_space(4))) Problem KProblem;
+
+// LDS of one phase unit: the stage ring, which after the main loop the
+// settling epilogues reuse as two store-staging regions per wave and the
+// tile's bias.
+template <typename OP, int BM, int BN> constexpr int phase_smem_bytes() {
+    using C = TileCfg<BM, BN, OpTraits<OP>::bytes>;
+    constexpr int STAGE_END = 2 * C::NWAVES * kStageWaveBytes + BN * 4;
+    return C::NS * C::stage_bytes > STAGE_END ? C::NS * C::stage_bytes : STAGE_END;
+}
+
+// One workgroup's share of a phase: virtual block `vblock` of a grid of
+// `vgrid` blocks over the `nprob` problems at `kprobs` (constant memory).
+// A launch of the phase runs it once per workgroup (vblock = blockIdx.x); a
+// persistent launch runs every virtual block of a phase, several per
+// workgroup, between grid barriers.  `smem` is the workgroup's LDS of
+// phase_smem_bytes() bytes.
 template <typename OP, int BM, int BN, int EPI>
-__global__ void __launch_bounds__((TileCfg<BM, BN>::NT), (TileCfg<BM, BN>::OCC))
-phase_kernel(const ProblemSet set, const PhaseArgs args) {
+__device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, const PhaseArgs& args, const int vblock,
+                                           const int vgrid, char* smem) {
     constexpr int OPB = OpTraits<OP>::bytes;
     using C = TileCfg<BM, BN, OPB>;
-    // The stage ring; after the main loop the settling epilogues reuse it as
-    // two store-staging regions per wave.
-    // two store-staging regions per wave and the tile's bias.
-    constexpr int STAGE_END = 2 * C::NWAVES * kStageWaveBytes + BN * 4;
-    constexpr int SMEM = C::NS * C::stage_bytes > STAGE_END ? C::NS * C::stage_bytes : STAGE_END;
-    __shared__ __attribute__((aligned(16))) char smem[SMEM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -496,17 +508,12 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     // Energy of the previous error phase, reduced per row in a fixed order
     // before any tile work (deterministic, no atomics).
     if (EPI == EPI_UPDATE && args.energy_out != nullptr) {
-        for (int row = blockIdx.x * C::NT + tid; row < args.batch; row += gridDim.x * C::NT) {
+        for (int row = vblock * C::NT + tid; row < args.batch; row += vgrid * C::NT) {
             gst(args.energy_out + (size_t)args.t * args.batch + row,
                 sum_slots(args.energy_part, args.ldp, args.nslots, row));
         }
     }
 
-    // `set` is the first kernel argument, so it sits at offset 0 of the kernarg
-    // segment: index the problems there (scalar loads from constant memory)
-    // instead of letting the compiler copy the whole set to scratch.
-    typedef const __attribute__((address_space(4))) Problem KProblem;
-    KProblem* kprobs = (KProblem*)__builtin_amdgcn_kernarg_segment_ptr();
     // XCD x runs the x-th eighth of every problem's tiles, problem after
     // problem.  Every XCD, and every CU of it (an XCD deals its workgroups
     // round-robin over its CUs), then gets a like share of the long-K and the
@@ -522,10 +529,10 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
     auto units_of = [&](int q) PCD_INLINE {
         return n_act < 0 ? kprobs[q].tiles : n_act * kprobs[q].tiles_n * max(kprobs[q].ksplit, 1);
     };
-    const int x = blockIdx.x % kXcds;
-    int i = blockIdx.x / kXcds, p = 0, local = -1;
+    const int x = vblock % kXcds;
+    int i = vblock / kXcds, p = 0, local = -1;
     if (args.tile_order == TILE_INTERLEAVED) {
-        for (; p < set.n; ++p) {
+        for (; p < nprob; ++p) {
             int lo, cnt;
             xcd_share(units_of(p), x, lo, cnt);
             if (i < cnt) {
@@ -536,12 +543,12 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
         }
     } else {
         int total = 0;
-        for (int q = 0; q < set.n; ++q) total += units_of(q);
+        for (int q = 0; q < nprob; ++q) total += units_of(q);
         int lo, cnt;
         xcd_share(total, x, lo, cnt);
         if (i < cnt) {
             int t = lo + i;
-            for (; p < set.n; ++p) {
+            for (; p < nprob; ++p) {
                 if (t < units_of(p)) {
                     local = t;
                     break;
@@ -1074,6 +1081,113 @@ phase_kernel(const ProblemSet set, const PhaseArgs args) {
                 }
             });
         });
+    }
+}
+
+// One phase launch: workgroup b runs virtual block b.  `set` is the first
+// kernel argument, so it sits at offset 0 of the kernarg segment: the problems
+// are indexed there (scalar loads from constant memory) instead of being
+// copied to scratch.
+template <typename OP, int BM, int BN, int EPI>
+__global__ void __launch_bounds__((TileCfg<BM, BN>::NT), (TileCfg<BM, BN>::OCC))
+phase_kernel(const ProblemSet set, const PhaseArgs args) {
+    __shared__ __attribute__((aligned(16))) char smem[phase_smem_bytes<OP, BM, BN>()];
+    phase_unit<OP, BM, BN, EPI>((KProblem*)__builtin_amdgcn_kernarg_segment_ptr(), set.n, args, blockIdx.x, gridDim.x,
+                                smem);
+}
+
+// ------------------------------------------------------- persistent settling
+
+// Grid barrier of a persistent launch.  `count` starts at zero and counts
+// arrivals over all barriers of the launch; `error` is set by a barrier that
+// gave up.
+struct GridSync {
+    int* count;
+    int* error;
+    int spin_limit;   // polls of the arrival count before a barrier gives up
+};
+
+// The k-th barrier (k from 1) of `nw` workgroups.  Every global write a
+// workgroup made before it is visible to every workgroup after it: each wave
+// waits for its own stores, the workgroup barrier joins the waves, thread 0's
+// device-scope fence writes them back past its XCD's L2 before the arrival is
+// counted, and its fence after the wait drops the CU's and the XCD's stale
+// lines before any wave reads again.  The count is read with device-scope
+// atomics (coherent across the XCDs).  A barrier that polls spin_limit times
+// without seeing all arrivals (or sees another's give-up) sets *error and
+// returns false; the caller then leaves the kernel, so every wave exits
+// normally.
+__device__ __forceinline__ bool grid_barrier(const GridSync& g, int k, int nw, int* ok) {
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        __hip_atomic_fetch_add(g.count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int target = k * nw;
+        int good = 1;
+        for (int spins = 0;; ++spins) {
+            if (__hip_atomic_load(g.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+            if (spins >= g.spin_limit || __hip_atomic_load(g.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                __hip_atomic_store(g.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                good = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        __threadfence();
+        *ok = good;
+    }
+    __syncthreads();
+    return *ok != 0;
+}
+
+// Everything one persistent settling needs, passed as the kernel's argument:
+// both phases' problems (first, so the kernel indexes them in the kernarg
+// segment as a phase launch does), the phases' arguments, their virtual
+// grids, the step count and the barrier.
+constexpr int kMaxPersistProblems = 6;
+struct PersistArgs {
+    Problem err_p[kMaxPersistProblems];
+    Problem upd_p[kMaxPersistProblems];
+    PhaseArgs err, upd;          // the phases' arguments; t is set per step
+    int err_n, upd_n;            // problems per phase
+    int err_grid, upd_grid;      // virtual blocks per phase (a phase launch's grid)
+    int steps;
+    GridSync sync;
+};
+
+// The T-step loop of a settling in one launch: every step runs all virtual
+// blocks of the error phase, a grid barrier, all of the update phase, a grid
+// barrier.  Workgroup w runs virtual blocks w, w + nw, ... of each phase (nw a
+// multiple of the XCD count, so that a virtual block shares an XCD with the
+// blocks its phase launch would have put beside it).  The units are the phase
+// kernels' own, so a settling computes exactly what the per-phase launches
+// compute.  The launch must be cooperative: every workgroup resident at once.
+static_assert(offsetof(PersistArgs, err_p) == 0, "the problems lead the kernel argument");
+template <typename OP, int BM, int BN>
+__global__ void __launch_bounds__((TileCfg<BM, BN>::NT), 1) persistent_relax_kernel(const PersistArgs pa) {
+    __shared__ __attribute__((aligned(16))) char smem[phase_smem_bytes<OP, BM, BN>()];
+    __shared__ int ok;
+    // `pa` is the only kernel argument: its problem arrays sit in the kernarg segment
+    KProblem* err_p = (KProblem*)__builtin_amdgcn_kernarg_segment_ptr();
+    KProblem* upd_p = err_p + kMaxPersistProblems;
+    const int w = blockIdx.x, nw = gridDim.x;
+    int k = 0;
+    for (int t = 0; t < pa.steps; ++t) {
+        PhaseArgs a = pa.err;
+        a.t = t;
+        for (int v = w; v < pa.err_grid; v += nw) {
+            phase_unit<OP, BM, BN, EPI_ERROR>(err_p, pa.err_n, a, v, pa.err_grid, smem);
+            __syncthreads();   // the next unit's loads reuse the LDS this one's epilogue read
+        }
+        if (!grid_barrier(pa.sync, ++k, nw, &ok)) return;
+        PhaseArgs u = pa.upd;
+        u.t = t;
+        for (int v = w; v < pa.upd_grid; v += nw) {
+            phase_unit<OP, BM, BN, EPI_UPDATE>(upd_p, pa.upd_n, u, v, pa.upd_grid, smem);
+            __syncthreads();
+        }
+        if (!grid_barrier(pa.sync, ++k, nw, &ok)) return;
     }
 }
 

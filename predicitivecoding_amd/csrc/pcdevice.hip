@@ -244,6 +244,9 @@ constexpr int kRowPad = 256;    // row dims padded to the widest tile
 constexpr int kKStaggerAuto = -1;
 int auto_k_stagger(int nk, bool one_row_tile = false);
 constexpr int kMaxKStagger = 64;
+// Persistent settling buffer: the grid barrier's arrival count and give-up flag.
+constexpr size_t kPersistBytes = 256;
+constexpr int kPersistSpinDefault = 1 << 22;   // about a second of polls (each a device-scope load and a sleep)
 
 struct Plan;
 
@@ -261,6 +264,7 @@ struct Workspace {
     int* split_count = nullptr;        // split-K finished-range counters, zero between launches
     int* act_tm = nullptr;             // ragged: row tiles still running at the current step [cap / 64]
     int* act_count = nullptr;          // ragged: their number
+    void* persist = nullptr;           // persistent settling: the grid barrier's arrival count and give-up flag
     void* rg_tables = nullptr;         // ragged: per-call tables (see pcd_pc_relax_ragged), sized for cap rows
     hipStream_t capture = nullptr;     // private stream used for graph capture
     std::vector<std::unique_ptr<Plan>> plans;
@@ -308,6 +312,9 @@ struct pcd_model {
     std::vector<std::unique_ptr<Workspace>> ws;
     // options
     int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED, split_k = 1;
+    int persistent = 0;                 // fixed-step fp32 settlings of few tiles as one persistent launch (opt-in)
+    int persist_spin = kPersistSpinDefault;
+    int persist_grid = 0;               // workgroups of the persistent launch (0: automatic)
     int k_stagger = 0;                  // settling phases: kKStaggerAuto (16-bit default), 0 off, or a fixed value
     int ragged_tiles = 1;               // ragged phases deal only the row tiles still running
     int ragged_order = 1;               // ragged requests settle in decreasing step budget (0: caller's order)
@@ -507,6 +514,7 @@ int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out
     if ((st = dev_alloc_zero(w->owned, (void**)&w->split_count, (size_t)split_part_tiles(m) * 4))) return st;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->act_tm, (size_t)(need / 64) * 4))) return st;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->act_count, 4))) return st;
+    if ((st = dev_alloc_zero(w->owned, &w->persist, kPersistBytes))) return st;
     HIP_TRY(hipStreamCreateWithFlags(&w->capture, hipStreamNonBlocking));
     *out = w;
     return PCD_SUCCESS;
@@ -607,6 +615,7 @@ struct RelaxSpec {
     Tile tile{0, 0};
     int clamp_top = 0;              // layer L-1 holds rows staged by the caller and is never updated
     int keep_hidden = 0;            // layers 1..L-2 start from rows staged by the caller, not from zero
+    int persistent = 0;             // the step loop as one persistent launch (see persistent_fits)
     float* energy_out = nullptr;    // [steps x batch] per-row energies (nullable)
     // ragged early exit (row_req null: fixed steps for every row)
     const int* row_req = nullptr;
@@ -647,6 +656,23 @@ int collect_timer(pcd_model* m, PhaseTimer& timer, hipStream_t s) {
     return PCD_SUCCESS;
 }
 
+// The phases' common arguments for a settling (t and energy_out are set per
+// launch).
+PhaseArgs relax_args(const pcd_model* m, const Workspace* w, const RelaxSpec& r, int nslots) {
+    PhaseArgs args = base_args(m, w, r.batch, nslots);
+    if (args.k_stagger == kKStaggerAuto) {
+        // the settling phases' longest K sweep at this tile (padded sizes are
+        // both phases' K)
+        const int maxp = *std::max_element(m->P.begin(), m->P.end());
+        args.k_stagger = auto_k_stagger(maxp / stage_k(m->dtype, r.tile), r.batch <= r.tile.m);
+    }
+    args.row_req = r.row_req;
+    args.done_at = r.done_at;
+    const bool need_energy = r.energy_out != nullptr || r.row_req != nullptr;
+    if (!need_energy) args.energy_part = nullptr;
+    return args;
+}
+
 // Zero the free states, FFG warm start (Network.cs:121-131), then the step
 // loop.  Layer 0 (and, with clamp_top, layer L-1) must already hold its rows.
 int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s, PhaseTimer* timer) {
@@ -663,17 +689,7 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
     std::vector<ProblemSet> err, upd;
     int nslots = 0;
     build_phase_sets(m, w, batch, tile, r.clamp_top, err, upd, &nslots);
-    PhaseArgs args = base_args(m, w, batch, nslots);
-    if (args.k_stagger == kKStaggerAuto) {
-        // the settling phases' longest K sweep at this tile (padded sizes are
-        // both phases' K)
-        const int maxp = *std::max_element(m->P.begin(), m->P.end());
-        args.k_stagger = auto_k_stagger(maxp / stage_k(m->dtype, tile), batch <= tile.m);
-    }
-    args.row_req = r.row_req;
-    args.done_at = r.done_at;
-    const bool need_energy = r.energy_out != nullptr || r.row_req != nullptr;
-    if (!need_energy) args.energy_part = nullptr;
+    const PhaseArgs args = relax_args(m, w, r, nslots);
 
     if (m->ffg) {
         for (int l = L - 1; l >= 2; --l) {
@@ -817,6 +833,70 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
     return w->plans.back().get();
 }
 
+// A fixed-step fp32 settling whose phases deal at most two workgroups per CU
+// (its launches, not its tiles, bound it) runs as one persistent launch:
+// option `persistent` on, no profiling, 64 x 64 tiles, and each phase's
+// problems fit the kernel argument.
+bool persistent_fits(const pcd_model* m, Tile tile, const std::vector<ProblemSet>& err,
+                     const std::vector<ProblemSet>& upd) {
+    if (!m->persistent || m->profile || m->dtype != PCD_F32 || tile.m != 64 || tile.n != 64) return false;
+    if (err.size() != 1 || upd.size() != 1) return false;
+    if (err[0].n > kMaxPersistProblems || upd[0].n > kMaxPersistProblems) return false;
+    const int lim = 2 * m->cus;
+    return phase_grid(err[0], m->tile_order) <= lim && phase_grid(upd[0], m->tile_order) <= lim;
+}
+
+// The settling r (fixed steps, no ragged rows) as one persistent launch, when
+// persistent_fits allows it; returns false (nothing enqueued) otherwise.  The
+// states are zeroed and the FFG sweep runs as in enqueue_relax, then
+// persistent_relax_kernel runs the step loop with grid barriers between the
+// phases.  The call waits for the settling and reads the barrier's give-up
+// flag: *status is PCD_HIP_ERROR if a barrier gave up.
+bool run_persistent(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s, int* status) {
+    std::vector<ProblemSet> err, upd;
+    int nslots = 0;
+    build_phase_sets(m, w, r.batch, r.tile, r.clamp_top, err, upd, &nslots);
+    if (!persistent_fits(m, r.tile, err, upd)) return false;
+    // workgroups of the launch: a multiple of the XCD count, all resident at once
+    const int cap = persistent_blocks_per_cu() * m->cus / kXcds * kXcds;
+    const int err_grid = phase_grid(err[0], m->tile_order), upd_grid = phase_grid(upd[0], m->tile_order);
+    int nw = m->persist_grid > 0 ? m->persist_grid : (std::max(err_grid, upd_grid) + kXcds - 1) / kXcds * kXcds;
+    if (nw > cap) nw = cap;
+    if (nw < kXcds) return false;   // the kernel cannot be resident (no occupancy)
+    // zero the free states and run the FFG sweep
+    RelaxSpec r0 = r;
+    r0.steps = 0;
+    if ((*status = enqueue_relax(m, w, r0, s, nullptr))) return true;
+    PersistArgs pa;
+    std::memset(&pa, 0, sizeof pa);
+    for (int i = 0; i < err[0].n; ++i) pa.err_p[i] = err[0].p[i];
+    for (int i = 0; i < upd[0].n; ++i) pa.upd_p[i] = upd[0].p[i];
+    pa.err = relax_args(m, w, r, nslots);
+    pa.upd = pa.err;
+    pa.err.energy_out = nullptr;
+    pa.upd.energy_out = r.energy_out;
+    pa.err_n = err[0].n;
+    pa.upd_n = upd[0].n;
+    pa.err_grid = err_grid;
+    pa.upd_grid = upd_grid;
+    pa.steps = r.steps;
+    int* sync = (int*)w->persist;
+    pa.sync.count = sync;
+    pa.sync.error = sync + 1;
+    pa.sync.spin_limit = m->persist_spin;
+    if ((*status = launch_zero(sync, kPersistBytes, s))) return true;
+    if ((*status = from_hip(launch_persistent_tile<float, 64, 64>(pa, nw, s), "persistent_relax_kernel launch")))
+        return true;
+    int flag = 0;
+    hipError_t e = hipMemcpyAsync(&flag, sync + 1, 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if ((*status = from_hip(e, "persistent settling")) != PCD_SUCCESS) return true;
+    if (flag)
+        *status = fail(PCD_HIP_ERROR, "persistent settling: a barrier gave up after %d polls (%d workgroups)",
+                       m->persist_spin, nw);
+    return true;
+}
+
 // A fixed-step settling of `batch` staged rows (layer 0, and the top with
 // clamp_top): eager with per-phase timing under the profile option, else the
 // cached graph of the T-step loop.  *energy receives the buffer holding the
@@ -831,6 +911,15 @@ int run_relax(pcd_model* m, Workspace* w, int batch, int steps, int clamp_top, i
     r.clamp_top = clamp_top;
     r.keep_hidden = keep_hidden;
     *energy = nullptr;
+    if (!want_energy || caller_energy) {
+        r.energy_out = want_energy ? caller_energy : nullptr;
+        int st = PCD_SUCCESS;
+        if (run_persistent(m, w, r, s, &st)) {
+            if (!st) *energy = r.energy_out;
+            return st;
+        }
+        r.energy_out = nullptr;
+    }
     if (m->profile || !m->use_graph) {
         float* buf = caller_energy;
         if (want_energy && !buf) return fail(PCD_INVALID_VALUE, "run_relax: energy buffer missing");
@@ -1421,6 +1510,15 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
             return fail(PCD_INVALID_VALUE, "tile_order must be 0 (interleaved) or 1 (contiguous)");
         m->tile_order = value;
     } else if (n == "ragged_tiles") m->ragged_tiles = value ? 1 : 0;
+    else if (n == "persistent") m->persistent = value ? 1 : 0;
+    else if (n == "persist_spin") {
+        if (value < 1) return fail(PCD_INVALID_VALUE, "persist_spin must be >= 1");
+        m->persist_spin = value;
+    } else if (n == "persist_grid") {
+        if (value < 0 || value % kXcds)
+            return fail(PCD_INVALID_VALUE, "persist_grid must be 0 or a multiple of %d", kXcds);
+        m->persist_grid = value;
+    }
     else if (n == "ragged_order") m->ragged_order = value ? 1 : 0;
     else if (n == "k_stagger") {
         if (value < kKStaggerAuto || value > kMaxKStagger)

@@ -35,4 +35,22 @@ hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& ar
 template hipError_t launch_phase_tile<InstOp, PCD_BM, PCD_BN>(int, const ProblemSet&, const PhaseArgs&, int,
                                                               hipStream_t);
 
+#if PCD_OP_ID == 0 && PCD_BM == 64 && PCD_BN == 64
+template <typename OP, int BM, int BN>
+hipError_t launch_persistent_tile(const PersistArgs& args, int grid, hipStream_t s) {
+    void* params[] = {(void*)&args};
+    return hipLaunchCooperativeKernel((const void*)persistent_relax_kernel<OP, BM, BN>, dim3(grid),
+                                      dim3(TileCfg<BM, BN>::NT), params, 0, s);
+}
+template hipError_t launch_persistent_tile<float, 64, 64>(const PersistArgs&, int, hipStream_t);
+
+int persistent_blocks_per_cu() {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)persistent_relax_kernel<float, 64, 64>,
+                                                     TileCfg<64, 64>::NT, 0) != hipSuccess)
+        return 0;
+    return n;
+}
+#endif
+
 }  // namespace pcd

@@ -16,6 +16,14 @@ namespace pcd {
 template <typename OP, int BM, int BN>
 hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t stream);
 
+// Launches persistent_relax_kernel<OP, BM, BN> cooperatively over `grid`
+// workgroups (fp32 64 x 64 is the instantiation the library builds).
+template <typename OP, int BM, int BN>
+hipError_t launch_persistent_tile(const PersistArgs& args, int grid, hipStream_t stream);
+extern template hipError_t launch_persistent_tile<float, 64, 64>(const PersistArgs&, int, hipStream_t);
+// Workgroups of persistent_relax_kernel<float, 64, 64> one CU holds at once.
+int persistent_blocks_per_cu();
+
 #define PCD_DECLARE_TILE(OP, BM, BN)                                                                    \
     extern template hipError_t launch_phase_tile<OP, BM, BN>(int, const ProblemSet&, const PhaseArgs&, int, \
                                                              hipStream_t);
