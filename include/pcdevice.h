@@ -381,6 +381,8 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *                0: in the caller's order.  fp32 results are the same.
  *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
  *                time every phase launch with HIP events (pcd_pc_profile_result)
+ *   split_min    fewest K stages a split-K range of a settling phase takes
+ *                (default 12; fewer gives more, shorter ranges)
  *   persistent   1: a fixed-step fp32 settling whose phases deal at most two
  *                workgroups per CU (64 x 64 tiles, at most 6 problems a phase)
  *                runs as one cooperative launch of the whole step loop, with

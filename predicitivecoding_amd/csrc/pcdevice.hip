@@ -244,6 +244,12 @@ constexpr int kRowPad = 256;    // row dims padded to the widest tile
 constexpr int kKStaggerAuto = -1;
 int auto_k_stagger(int nk, bool one_row_tile = false);
 constexpr int kMaxKStagger = 64;
+// Fewest K stages a split-K range runs: a range also pays its partial tile's
+// store, the count and (last range) the reduction, a few microseconds.
+#ifndef PCD_SPLIT_MIN_STAGES
+#define PCD_SPLIT_MIN_STAGES 12
+#endif
+constexpr int kSplitMinStages = PCD_SPLIT_MIN_STAGES;
 // Persistent settling buffer: the grid barrier's arrival count and give-up flag.
 constexpr size_t kPersistBytes = 256;
 constexpr int kPersistSpinDefault = 1 << 22;   // about a second of polls (each a device-scope load and a sleep)
@@ -313,6 +319,7 @@ struct pcd_model {
     // options
     int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED, split_k = 1;
     int persistent = 0;                 // fixed-step fp32 settlings of few tiles as one persistent launch (opt-in)
+    int split_min = kSplitMinStages;    // fewest K stages of a split-K range in the settling phases
     int persist_spin = kPersistSpinDefault;
     int persist_grid = 0;               // workgroups of the persistent launch (0: automatic)
     int k_stagger = 0;                  // settling phases: kKStaggerAuto (16-bit default), 0 off, or a fixed value
@@ -404,12 +411,6 @@ int max_energy_slots(const pcd_model* m) {
 // scratch holds `cus` partial tiles of 128 x 128 and as many counters.
 int split_part_tiles(const pcd_model* m) { return std::max(m->cus, 1); }
 
-// Fewest K stages a split-K range runs: a range also pays its partial tile's
-// store, the count and (last range) the reduction, a few microseconds.
-#ifndef PCD_SPLIT_MIN_STAGES
-#define PCD_SPLIT_MIN_STAGES 12
-#endif
-constexpr int kSplitMinStages = PCD_SPLIT_MIN_STAGES;
 
 int split_factor(int cus, int split_k, long tiles, Tile tile) {
     if (!split_k || tile.m * tile.n > 128 * 128 || tiles < 1 || tiles * 2 > cus) return 1;
@@ -446,7 +447,8 @@ struct SplitScratch {
 // per CU: its tiles would otherwise give a part of the CUs one more whole tile
 // than the rest (c2's update phase: 8 tiles of the 256-wide layer per XCD of 32
 // CUs next to 3 x 32 full tiles).  Splitting stops where the scratch is spent.
-void assign_split(int cus, int split_k, int dtype, Tile tile, const SplitScratch& sc, std::vector<ProblemSet>& sets) {
+void assign_split(int cus, int split_k, int dtype, Tile tile, const SplitScratch& sc, std::vector<ProblemSet>& sets,
+                  int min_stages = kSplitMinStages) {
     long tiles = 0;
     for (auto& ps : sets)
         for (int i = 0; i < ps.n; ++i) tiles += (long)ps.p[i].tiles_m * ps.p[i].tiles_n;
@@ -460,7 +462,7 @@ void assign_split(int cus, int split_k, int dtype, Tile tile, const SplitScratch
             const int t = p.tiles_m * p.tiles_n;
             const int share = (t + kXcds - 1) / kXcds;
             const int fb = (split_k && small_tile && share < per_xcd) ? per_xcd / share : 1;
-            int ks = std::max(1, std::min({std::max(f, fb), kMaxSplit, p.K / stage_k(dtype, tile) / kSplitMinStages}));
+            int ks = std::max(1, std::min({std::max(f, fb), kMaxSplit, p.K / stage_k(dtype, tile) / min_stages}));
             if (ks > 1 && units + (long)t * ks > sc.budget) ks = 1;
             p.ksplit = ks;
             p.tiles = t * ks;
@@ -584,8 +586,8 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
     sc.part = w->split_part;
     sc.count = w->split_count;
     sc.budget = split_part_tiles(m);
-    assign_split(m->cus, m->split_k, m->dtype, tile, sc, err);
-    assign_split(m->cus, m->split_k, m->dtype, tile, sc, upd);
+    assign_split(m->cus, m->split_k, m->dtype, tile, sc, err, m->split_min);
+    assign_split(m->cus, m->split_k, m->dtype, tile, sc, upd, m->split_min);
     *nslots = slot;
 }
 
@@ -1511,6 +1513,10 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
         m->tile_order = value;
     } else if (n == "ragged_tiles") m->ragged_tiles = value ? 1 : 0;
     else if (n == "persistent") m->persistent = value ? 1 : 0;
+    else if (n == "split_min") {
+        if (value < 1) return fail(PCD_INVALID_VALUE, "split_min must be >= 1");
+        m->split_min = value;
+    }
     else if (n == "persist_spin") {
         if (value < 1) return fail(PCD_INVALID_VALUE, "persist_spin must be >= 1");
         m->persist_spin = value;
