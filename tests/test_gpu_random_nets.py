@@ -152,3 +152,47 @@ def test_random_learn(oracle, seed):
                 energy=max_rel(en, ren))
     print(" ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
     assert all(v < 1e-4 for v in errs.values()), errs
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_deep_network_spans_several_launches(oracle, dtype):
+    # 21 levels: each phase has 20 problems, more than one grouped launch holds
+    # (16), so every phase runs as two launches; relax, classify, the ragged
+    # path with an exit and (fp32) the learning step all go through them
+    rng = np.random.default_rng(77)
+    sizes = [int(v) for v in rng.choice([16, 33, 64, 70], size=21)]
+    sizes[-1] = 5
+    snap, W, b, P, x = build_case(sizes, "tanh", 0.05, seed=77, init="fanin", bias_scale=0.1, batch=70)
+    tol = TOL[dtype]
+    top, st, en = run_gpu(snap, x, 6, dtype=dtype, states=True, energy=True)
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 6, dtype=dtype, states=True, energy=True)
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren), states=max(max_rel(a, r) for a, r in zip(st, rst)))
+    print("relax", " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+    assert all(v < tol for v in errs.values()), errs
+    m = PcDeviceModel(snap, dtype)
+    try:
+        ce, cls, be = m.classify(x[:9], 4)
+        offs = np.array([0, 3, 40, 70], np.int32)
+        steps = np.array([5, 9, 2], np.int32)
+        used, fe, rtop2 = m.relax_ragged(x, offs, steps, "relative", 0.05) if dtype == "f32" else (None, None, None)
+    finally:
+        m.close()
+    rce, rcls, _ = oracle.classify(sizes, "tanh", 0.05, W, b, P, x[:9], 4, round_mode=ROUND[dtype])
+    assert max_rel(ce, rce) < tol
+    if dtype == "f32":
+        rused, rfe, rrtop = oracle.ragged_relax(sizes, "tanh", 0.05, W, b, P, x, offs, steps, exit_rule="relative",
+                                                exit_thr=0.05)
+        print("used", used.tolist(), "oracle", rused.tolist(), flush=True)
+        assert np.array_equal(used, rused)
+        assert max_rel(fe, rfe) < tol and max_rel(rtop2, rrtop) < tol
+        y = np.eye(5, dtype=np.float32)[np.arange(70) % 5]
+        m = PcDeviceModel(snap, "f32")
+        try:
+            en_learn = m.learn(x, y, 4, 0.02)
+            gw, gb = m.get_weights()
+        finally:
+            m.close()
+        rw, rb, ren2 = oracle.learn(sizes, "tanh", 0.05, W, b, P, x, y, 4, 0.02)
+        assert max(max_rel(a, r) for a, r in zip(gw, rw)) < 1e-4
+        assert max(max_rel(a, r) for a, r in zip(gb, rb)) < 1e-4
+        assert max_rel(en_learn, ren2) < 1e-4
