@@ -18,6 +18,21 @@ def test_library_exports_every_declared_symbol():
     assert set(syms) == set(_native._SIGNATURES), set(syms) ^ set(_native._SIGNATURES)
 
 
+def test_header_is_plain_c_and_the_c_client_links(tmp_path):
+    # include/pcdevice.h is the whole boundary for a C caller: the C99 client
+    # compiles with -pedantic and links against the library and the oracle
+    import os
+    import subprocess
+    here = os.path.dirname(os.path.abspath(__file__))
+    src = os.path.join(here, "c_client", "relax_client.c")
+    root = os.path.dirname(here)
+    out = str(tmp_path / "relax_client")
+    res = subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I" + os.path.join(root, "include"),
+                          src, "-o", out, "-L" + os.path.join(root, "predicitivecoding_amd"), "-lpcdevice_hip",
+                          "-L" + os.path.join(root, "oracle"), "-lpcoracle", "-lm"], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+
+
 def test_status_codes_match_reference_enum():
     # Interop/CudaStatus.cs:7-19
     want = {"Success": 0, "NotInitialized": 1, "NoDevice": 2, "OutOfMemory": 3, "InvalidValue": 4,
