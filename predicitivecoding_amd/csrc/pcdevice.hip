@@ -410,6 +410,8 @@ int max_energy_slots(const pcd_model* m) {
 // runs the epilogue.  Units of a phase never exceed the CU count, so the
 // scratch holds `cus` partial tiles of 128 x 128 and as many counters.
 int split_part_tiles(const pcd_model* m) { return std::max(m->cus, 1); }
+// Bytes of the split-K counters, whole 16-byte units so a zero kernel covers them.
+size_t split_count_bytes(const pcd_model* m) { return round_up((size_t)split_part_tiles(m) * 4, 16); }
 
 
 int split_factor(int cus, int split_k, long tiles, Tile tile) {
@@ -513,7 +515,7 @@ int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out
     if ((st = dev_alloc_zero(w->owned, (void**)&w->energy_part, (size_t)slots * need * 4))) return st;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->split_part, (size_t)split_part_tiles(m) * 128 * 128 * 4)))
         return st;
-    if ((st = dev_alloc_zero(w->owned, (void**)&w->split_count, (size_t)split_part_tiles(m) * 4))) return st;
+    if ((st = dev_alloc_zero(w->owned, (void**)&w->split_count, split_count_bytes(m)))) return st;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->act_tm, (size_t)(need / 64) * 4))) return st;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->act_count, 4))) return st;
     if ((st = dev_alloc_zero(w->owned, &w->persist, kPersistBytes))) return st;
@@ -893,9 +895,17 @@ bool run_persistent(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t 
     hipError_t e = hipMemcpyAsync(&flag, sync + 1, 4, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if ((*status = from_hip(e, "persistent settling")) != PCD_SUCCESS) return true;
-    if (flag)
-        *status = fail(PCD_HIP_ERROR, "persistent settling: a barrier gave up after %d polls (%d workgroups)",
-                       m->persist_spin, nw);
+    if (flag) {
+        // Workgroups that left at a barrier skipped their units, while others
+        // that saw every arrival went on: a split tile may have some of its
+        // ranges counted and never reach the range that resets its counter.
+        // The counters must read zero for the next launch of any kind.
+        int zst = launch_zero(w->split_count, split_count_bytes(m), s);
+        if (!zst) zst = from_hip(hipStreamSynchronize(s), "split counter reset");
+        *status = zst ? zst
+                      : fail(PCD_HIP_ERROR, "persistent settling: a barrier gave up after %d polls (%d workgroups)",
+                             m->persist_spin, nw);
+    }
     return true;
 }
 
@@ -1646,7 +1656,7 @@ size_t carve_workspace(const pcd_model* m, char* base, int batch, Tile tile, Wor
     }
     w.slots_cap = energy_slots(m, tile);
     w.energy_part = (float*)take((size_t)w.slots_cap * cap * 4);
-    w.split_count = (int*)take((size_t)split_part_tiles(m) * 4);
+    w.split_count = (int*)take(split_count_bytes(m));
     w.split_part = (float*)(base + off);
     std::vector<ProblemSet> err, upd;
     int nslots = 0;

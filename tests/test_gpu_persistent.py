@@ -81,12 +81,21 @@ def test_persistent_barrier_gives_up_and_recovers(oracle):
         with pytest.raises(DeviceException) as ei:
             m.relax(x, 20)
         assert ei.value.code == 5 and "gave up" in str(ei.value)
+        # a give-up can leave a split tile's ranges half counted; the next
+        # call, persistent or not, must still settle correctly
         m.set_option("persist_spin", 1 << 22)
         top, _, en = m.relax(x, 20, want_energy=True)
+        with pytest.raises(DeviceException):
+            m.set_option("persist_spin", 1)
+            m.relax(x, 20)
+        m.set_option("persist_spin", 1 << 22)
+        m.set_option("persistent", 0)
+        top0, _, en0 = m.relax(x, 20, want_energy=True)
     finally:
         m.close()
     rtop, _, ren = run_oracle(oracle, snap, W, b, P, x, 20, energy=True)
     assert max_rel(top, rtop) < 1e-4 and max_rel(en, ren) < 1e-4
+    assert max_rel(top0, rtop) < 1e-4 and max_rel(en0, ren) < 1e-4
 
 
 def test_persistent_grid_options():
