@@ -196,3 +196,41 @@ def test_deep_network_spans_several_launches(oracle, dtype):
         assert max(max_rel(a, r) for a, r in zip(gw, rw)) < 1e-4
         assert max(max_rel(a, r) for a, r in zip(gb, rb)) < 1e-4
         assert max_rel(en_learn, ren2) < 1e-4
+
+
+OPTION_SETS = [
+    {},
+    {"tile_order": 1},
+    {"split_min": 2},
+    {"split_min": 40},
+    {"split_k": 0},
+    {"use_graph": 0},
+    {"k_stagger": 0},
+    {"profile": 1},
+    {"tile_order": 1, "split_min": 2, "use_graph": 0, "k_stagger": 5},
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("opts", OPTION_SETS, ids=lambda o: "-".join(f"{k}{v}" for k, v in o.items()) or "defaults")
+def test_relaxation_options_keep_parity(oracle, dtype, opts):
+    # a 64-row batch on a network with a long K sweep, so the split-K paths and
+    # several problems per phase are in play; every option combination settles
+    # to the oracle's result
+    snap, W, b, P, x = build_case([300, 1030, 260, 70], "gelu", 0.08, batch=64, seed=41, init="fanin",
+                                  bias_scale=0.1)
+    m = PcDeviceModel(snap, dtype)
+    try:
+        for k, v in opts.items():
+            m.set_option(k, v)
+        top, st, en = m.relax(x, 7, want_states=True, want_energy=True)
+        prof = m.profile_result() if opts.get("profile") else None
+    finally:
+        m.close()
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 7, dtype=dtype, states=True, energy=True)
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren), states=max(max_rel(a, r) for a, r in zip(st, rst)))
+    print(opts, " ".join(f"{k}={v:.2e}" for k, v in errs.items()), prof, flush=True)
+    assert all(v < TOL[dtype] for v in errs.values()), errs
+    if prof is not None:
+        err_ms, upd_ms, launches = prof
+        assert launches == 7 and err_ms > 0 and upd_ms > 0
