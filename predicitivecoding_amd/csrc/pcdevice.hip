@@ -457,15 +457,28 @@ void assign_split(int cus, int split_k, int dtype, Tile tile, const SplitScratch
     const int f = split_factor(cus, split_k, tiles, tile);
     const int per_xcd = std::max(1, cus / kXcds);
     const bool small_tile = tile.m * tile.n <= 128 * 128;
+    auto wanted = [&](const Problem& p) {
+        const int t = p.tiles_m * p.tiles_n;
+        const int share = (t + kXcds - 1) / kXcds;
+        const int fb = (split_k && small_tile && share < per_xcd) ? per_xcd / share : 1;
+        return std::max(1, std::min({std::max(f, fb), kMaxSplit, p.K / stage_k(dtype, tile) / min_stages}));
+    };
+    // All or nothing: a phase whose splits do not all fit the scratch splits
+    // none of its problems (splitting only the first ones would leave those
+    // slower than the rest: c5s's phases, 11 problems of 16 tiles per XCD).
+    long need = 0;
+    for (auto& ps : sets)
+        for (int i = 0; i < ps.n; ++i) {
+            const int ks = wanted(ps.p[i]);
+            if (ks > 1) need += (long)ps.p[i].tiles_m * ps.p[i].tiles_n * ks;
+        }
+    const bool fits = need <= sc.budget;
     long units = 0, counters = 0;
     for (auto& ps : sets)
         for (int i = 0; i < ps.n; ++i) {
             Problem& p = ps.p[i];
             const int t = p.tiles_m * p.tiles_n;
-            const int share = (t + kXcds - 1) / kXcds;
-            const int fb = (split_k && small_tile && share < per_xcd) ? per_xcd / share : 1;
-            int ks = std::max(1, std::min({std::max(f, fb), kMaxSplit, p.K / stage_k(dtype, tile) / min_stages}));
-            if (ks > 1 && units + (long)t * ks > sc.budget) ks = 1;
+            const int ks = fits ? wanted(p) : 1;
             p.ksplit = ks;
             p.tiles = t * ks;
             if (ks > 1) {
