@@ -348,14 +348,21 @@ template <int BM, int BN, int OPB = 4> struct TileCfg {
     // line of every weight row per stage, which is what streams best from HBM
     // when the batch is small (the weights dominate the traffic).
     static constexpr bool BIG = BM == 256 && BN == 256;
-    static constexpr int WM = 2, WN = BIG ? 4 : 2;
-    static constexpr int NWAVES = WM * WN, NT = 64 * NWAVES;
+    // 32 x 32 (fp32 only) is one output block whose K the 4 waves share: each
+    // stage holds 64 K elements per row and wave w takes the w-th quarter of
+    // every stage, so a tile's K sweep takes a quarter of the MFMA issue time
+    // of a 64 x 64 tile's.  The waves' sums meet in LDS after the loop.
+    static constexpr bool KSW = BM == 32 && BN == 32;
+    static constexpr int KW = KSW ? 4 : 1;                 // waves sharing one block's K
+    static constexpr int WM = KSW ? 1 : 2, WN = BIG ? 4 : KSW ? 1 : 2;
+    static constexpr int NWAVES = WM * WN * KW, NT = 64 * NWAVES;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
     static constexpr bool MID = BM == 128 && BN == 128;
-    static constexpr int RB = BIG ? PCD_BIG_RB : MID ? PCD_MID_RB : (BM == 64 && OPB == 2) ? PCD_SMALL_RB16 : PCD_SMALL_RB;   // K bytes per row per stage
+    static constexpr int RB = BIG ? PCD_BIG_RB : MID ? PCD_MID_RB : KSW ? 256 : (BM == 64 && OPB == 2) ? PCD_SMALL_RB16 : PCD_SMALL_RB;   // K bytes per row per stage
     static constexpr int UNITS = RB / 16;                  // 16-byte units per row
     static constexpr int NC = RB / 32;                     // 32-byte MFMA chunks per stage
+    static constexpr int NCW = NC / KW;                    // chunks of a stage one wave takes
     static constexpr int stage_bytes = (BM + BN) * RB;
     static constexpr int NS_WANT = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : (BM + BN >= 320) ? 3 : PCD_SMALL_NS;
     static constexpr int NS = BIG ? NS_WANT : (NS_WANT * stage_bytes <= 80 * 1024 ? NS_WANT : 80 * 1024 / stage_bytes);   // stages in the LDS ring
@@ -365,7 +372,8 @@ template <int BM, int BN, int OPB = 4> struct TileCfg {
     static constexpr int QPW = (BM + BN) / ROWS_PER_LOAD / NWAVES;   // loads per wave per stage
     static_assert(FM >= 1 && FN >= 1 && QPW >= 1, "tile too small");
     static_assert((BM + BN) % (NWAVES * ROWS_PER_LOAD) == 0, "stage rows must split evenly over the waves");
-    static_assert(NC % 2 == 0, "fragment buffers alternate within a stage");
+    static_assert(NCW % 2 == 0, "fragment buffers alternate within a stage");
+    static_assert(!KSW || OPB == 4, "the 32 x 32 tile takes fp32 operands");
     static_assert(D >= 1 && D * QPW < 64, "stage_ready waits on at most 63 loads");
     static_assert(NS * stage_bytes <= 160 * 1024, "LDS ring exceeds the 160 KB of a CU");
     static_assert(64 % (RB / OPB) == 0, "K is padded to 64 elements: a stage's K must divide it");
@@ -503,7 +511,13 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / C::WN, wn = wave % C::WN;
+    // Wave w of a K-shared tile takes chunks [w NCW, (w + 1) NCW) of every
+    // stage and the whole block; the other tiles give each wave its own block.
+    const int wk = C::KW > 1 ? wave : 0, wmn = C::KW > 1 ? 0 : wave;
+    const int wm = wmn / C::WN, wn = wmn % C::WN;
+    // Waves that store the tile's results (a K-shared tile's waves all hold the
+    // same sums after the reduction; wave 0 stores them).
+    const bool writer = C::KW == 1 || wave == 0;
 
     // Energy of the previous error phase, reduced per row in a fixed order
     // before any tile work (deterministic, no atomics).
@@ -697,7 +711,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         });
         __syncthreads();
     };
-    constexpr int NC = C::NC;
+    constexpr int NC = C::NCW;   // chunks of a stage this wave reads
     u32x4 fa[2][C::FM], fb[2][C::FN];
     // One LDS fragment read after each of the chunk's first MFMAs, the rest of
     // the MFMAs after them.
@@ -712,9 +726,10 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         });
         if constexpr (NMF > NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
     };
+    const int c0 = wk * C::NCW;   // this wave's first chunk of a stage
     for (int s2 = 0; s2 < C::D && s2 < nk; ++s2) issue_stage(s2);
     stage_ready(0);
-    read_frags(0, 0, fa[0], fb[0]);
+    read_frags(0, c0, fa[0], fb[0]);
     // Chunk c's MFMAs run while chunk c+1's fragments are read; the last chunk
     // of a stage runs after the barrier that publishes the next stage, whose
     // first fragments it overlaps.  The last stage is peeled off.
@@ -723,10 +738,10 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         static_for<0, NC>([&](auto Cc) PCD_INLINE {
             constexpr int c = decltype(Cc)::value;
             if constexpr (c + 1 < NC) {
-                read_frags(kt % C::NS, c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
+                read_frags(kt % C::NS, c0 + c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
             } else {
                 stage_ready(kt + 1);
-                read_frags((kt + 1) % C::NS, 0, fa[0], fb[0]);
+                read_frags((kt + 1) % C::NS, c0, fa[0], fb[0]);
             }
             mfmas(fa[c & 1], fb[c & 1]);
             interleave();
@@ -734,7 +749,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     }
     static_for<0, NC>([&](auto Cc) PCD_INLINE {
         constexpr int c = decltype(Cc)::value;
-        if constexpr (c + 1 < NC) read_frags((nk - 1) % C::NS, c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
+        if constexpr (c + 1 < NC) read_frags((nk - 1) % C::NS, c0 + c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
         mfmas(fa[c & 1], fb[c & 1]);
     });
     static_for<1, NSPLIT>([&](auto Kc) PCD_INLINE {
@@ -744,6 +759,24 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             for (int j = 0; j < C::FN; ++j) accs[0][i][j] += accs[decltype(Kc)::value][i][j];
     });
     f32x16 (&acc)[C::FM][C::FN] = accs[0];
+    if constexpr (C::KW > 1) {
+        // The waves' partial sums of the block meet in LDS (lane-contiguous,
+        // conflict-free); every wave adds them in wave order, so all of them
+        // hold the same block.
+        float* red = (float*)smem;
+        __syncthreads();   // every wave is done reading the stage ring
+        static_for<0, 16>([&](auto R) PCD_INLINE {
+            constexpr int r = decltype(R)::value;
+            red[(wave * 16 + r) * 64 + lane] = acc[0][0][r];
+        });
+        __syncthreads();
+        static_for<0, 16>([&](auto R) PCD_INLINE {
+            constexpr int r = decltype(R)::value;
+            float v = red[r * 64 + lane];
+            static_for<1, C::KW>([&](auto W) PCD_INLINE { v += red[(decltype(W)::value * 16 + r) * 64 + lane]; });
+            acc[0][0][r] = v;
+        });
+    }
 
     // ---- split-K: publish this range's partial tile; the range that finishes
     // last sums all of them in range order (the same sum whichever finishes
@@ -769,19 +802,22 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         // accumulators as 8 consecutive 64-bit pairs (a wave's block is 4 KB).
         typedef unsigned long long u64;
         u64* part = (u64*)(P.part + (size_t)tile * ks * (BM * BN));
-        auto slot_of = [&](int i, int j) PCD_INLINE { return (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 8; };
+        auto slot_of = [&](int i, int j) PCD_INLINE { return (((wmn * C::FM + i) * C::FN + j) * 64 + lane) * 8; };
         constexpr int UNIT = BM * BN / 2;   // 64-bit words of one partial tile
         u64* mine = part + (size_t)split * UNIT;
-        static_for<0, C::FM>([&](auto I) PCD_INLINE {
-            static_for<0, C::FN>([&](auto J) PCD_INLINE {
-                constexpr int i = decltype(I)::value, j = decltype(J)::value;
-                static_for<0, 8>([&](auto Q) PCD_INLINE {
-                    constexpr int q = decltype(Q)::value;
-                    const u64 w = (u64)__float_as_uint(acc[i][j][2 * q]) | ((u64)__float_as_uint(acc[i][j][2 * q + 1]) << 32);
-                    __hip_atomic_store(mine + slot_of(i, j) + q, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (writer) {
+            static_for<0, C::FM>([&](auto I) PCD_INLINE {
+                static_for<0, C::FN>([&](auto J) PCD_INLINE {
+                    constexpr int i = decltype(I)::value, j = decltype(J)::value;
+                    static_for<0, 8>([&](auto Q) PCD_INLINE {
+                        constexpr int q = decltype(Q)::value;
+                        const u64 w =
+                            (u64)__float_as_uint(acc[i][j][2 * q]) | ((u64)__float_as_uint(acc[i][j][2 * q + 1]) << 32);
+                        __hip_atomic_store(mine + slot_of(i, j) + q, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    });
                 });
             });
-        });
+        }
         wait_vmcnt<0>();      // this lane's partial stores are complete
         __syncthreads();      // ... every lane's; the stage ring is no longer read
         int* flag = (int*)smem;
@@ -940,14 +976,14 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
                     stage_group<OPB>(wstage2, g, dv, PackOp<OP>{});
                 });
                 const int brow = row0 + wm * C::WTM + i * 32, bcol = col0 + wn * C::WTN + j * 32;
-                if (P.eout) flush_block<4>(wstage, P.eout, ldo, brow, bcol, rmask, P.N, full);
-                flush_block<OPB>(wstage2, P.dout, ldo, brow, bcol, rmask, P.N, full);
+                if (P.eout && writer) flush_block<4>(wstage, P.eout, ldo, brow, bcol, rmask, P.N, full);
+                if (writer) flush_block<OPB>(wstage2, P.dout, ldo, brow, bcol, rmask, P.N, full);
                 if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
                 if constexpr (j == C::FN - 1) {
                     if (want_energy) {
                         // The two half-waves hold the two column halves of each group.
                         const float v = esum + __shfl_xor(esum, 32);
-                        if (half == 0 && row < P.M) {
+                        if (half == 0 && row < P.M && writer) {
                             const int slot = P.slot_base + tn * C::WN + wn;
                             gst(args.energy_part + (size_t)slot * args.ldp + row, v);
                         }
@@ -1013,12 +1049,13 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
                 if (P.mop) stage_group<OPB>(wstage2, g, mn, PackOp<OP>{});
             });
             const int brow = row0 + wm * C::WTM + i * 32, bcol = col0 + wn * C::WTN + j * 32;
-            flush_block<4>(wstage, P.m, ldo, brow, bcol, rmask, P.N, full);
-            if (P.mop) flush_block<OPB>(wstage2, P.mop, ldo, brow, bcol, rmask, P.N, full);
+            if (writer) flush_block<4>(wstage, P.m, ldo, brow, bcol, rmask, P.N, full);
+            if (P.mop && writer) flush_block<OPB>(wstage2, P.mop, ldo, brow, bcol, rmask, P.N, full);
             if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
             __builtin_amdgcn_sched_barrier(0);
         });
     } else if constexpr (EPI == EPI_FFG) {
+        if (!writer) return;   // no barrier follows
         static_for<0, C::FM>([&](auto I) PCD_INLINE {
             constexpr int i = decltype(I)::value;
             static_for<0, C::FN>([&](auto J) PCD_INLINE {
@@ -1041,6 +1078,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             });
         });
     } else {  // EPI_PLAIN: C = alpha acc + beta C
+        if (!writer) return;   // no barrier follows
         const float alpha = args.alpha, beta = args.beta;
         static_for<0, C::FM>([&](auto I) PCD_INLINE {
             constexpr int i = decltype(I)::value;

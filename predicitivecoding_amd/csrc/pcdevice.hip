@@ -168,13 +168,15 @@ int launch_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid,
 struct Tile {
     int m, n;
 };
-bool tile_supported(Tile t) {
-    return (t.m == 64 && (t.n == 64 || t.n == 128 || t.n == 256)) || (t.m == 128 && t.n == 128) ||
-           (t.m == 256 && t.n == 128) || (t.m == 256 && t.n == 256);
+bool tile_supported(Tile t, int dtype) {
+    return (t.m == 32 && t.n == 32 && dtype == PCD_F32) || (t.m == 64 && (t.n == 64 || t.n == 128 || t.n == 256)) ||
+           (t.m == 128 && t.n == 128) || (t.m == 256 && t.n == 128) || (t.m == 256 && t.n == 256);
 }
 
 template <typename OP>
 int launch_op(Tile tile, int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
+    if constexpr (std::is_same<OP, float>::value)
+        if (tile.m == 32 && tile.n == 32) return launch_tile<OP, 32, 32>(epi, set, args, grid, s);
     if (tile.m == 64 && tile.n == 64) return launch_tile<OP, 64, 64>(epi, set, args, grid, s);
     if (tile.m == 64 && tile.n == 128) return launch_tile<OP, 64, 128>(epi, set, args, grid, s);
     if (tile.m == 64 && tile.n == 256) return launch_tile<OP, 64, 256>(epi, set, args, grid, s);
@@ -230,6 +232,7 @@ inline int op_bytes(int dtype) { return dtype == PCD_F32 ? 4 : 2; }
 
 constexpr int kFeatPad = 64;    // feature dims padded to the deepest LDS stage (64 elements)
 constexpr int kRowPad = 256;    // row dims padded to the widest tile
+constexpr int kMinTileM = 32;   // rows of the shortest tile
 // K stagger of the settling phases and GEMMs with 16-bit operands: spreads
 // the tiles that share operand rows over 16 stage offsets (measured on 6 x 4096
 // and 12 x 8192 bf16 networks: 7-10% faster than no stagger, and better than 4
@@ -268,7 +271,7 @@ struct Workspace {
     int slots_cap = 0;
     float* split_part = nullptr;       // split-K partial tiles, kSplitPartTiles x 128 x 128 fp32
     int* split_count = nullptr;        // split-K finished-range counters, zero between launches
-    int* act_tm = nullptr;             // ragged: row tiles still running at the current step [cap / 64]
+    int* act_tm = nullptr;             // ragged: row tiles still running at the current step [cap / kMinTileM]
     int* act_count = nullptr;          // ragged: their number
     void* persist = nullptr;           // persistent settling: the grid barrier's arrival count and give-up flag
     void* rg_tables = nullptr;         // ragged: per-call tables (see pcd_pc_relax_ragged), sized for cap rows
@@ -362,9 +365,15 @@ long error_phase_tiles(const pcd_model* m, int batch, Tile t) {
 // The largest tile that still gives every CU at least two workgroups per
 // phase (a phase with fewer tiles leaves SIMDs idle: 64 x 64 beats 128 x 128
 // by 8% on the 1024-wide fp32 configuration).  256 x 256 only for 16-bit
-// operands with every layer at least 1024 wide.
+// operands with every layer at least 1024 wide.  An fp32 settling whose
+// error phase has fewer 64 x 64 tiles than the GPU has CUs takes the K-shared
+// 32 x 32 tile: its phases are bound by one tile's K sweep, which that tile
+// runs four times as fast (784-256-256-10 at a batch of 64: +43%), unless the
+// persistent form, built on 64 x 64, is asked for.
 Tile choose_tile(const pcd_model* m, int batch) {
     if (m->tile_m > 0) return Tile{m->tile_m, m->tile_n};
+    if (m->dtype == PCD_F32 && !m->persistent && error_phase_tiles(m, batch, Tile{64, 64}) < m->cus)
+        return Tile{32, 32};
     // A batch that fits one 64-row tile: any taller tile is mostly padding rows
     // (its MFMAs and its state loads wasted), and the phases stream weights.
     if (batch <= 64) return Tile{64, 64};
@@ -380,6 +389,7 @@ Tile choose_tile(const pcd_model* m, int batch) {
 
 // Energy partial slots a tile column owns: one per wave column of the tile.
 int slots_per_tile_n(Tile t) {
+    if (t.m == 32 && t.n == 32) return energy_slots_per_tile_n<32, 32>();
     if (t.m == 256 && t.n == 256) return energy_slots_per_tile_n<256, 256>();
     if (t.m == 256 && t.n == 128) return energy_slots_per_tile_n<256, 128>();
     if (t.m == 128 && t.n == 128) return energy_slots_per_tile_n<128, 128>();
@@ -397,7 +407,7 @@ int energy_slots(const pcd_model* m, Tile tile) {
 
 // The most slots any supported tile needs (sizes the workspace once).
 int max_energy_slots(const pcd_model* m) {
-    const Tile tiles[] = {{64, 64}, {64, 128}, {64, 256}, {128, 128}, {256, 128}, {256, 256}};
+    const Tile tiles[] = {{32, 32}, {64, 64}, {64, 128}, {64, 256}, {128, 128}, {256, 128}, {256, 256}};
     int slots = 0;
     for (Tile t : tiles) slots = std::max(slots, energy_slots(m, t));
     return slots;
@@ -421,6 +431,8 @@ int split_factor(int cus, int split_k, long tiles, Tile tile) {
 
 // K elements of one LDS stage of `tile` for an operand type.
 template <int OPB> int stage_rb(Tile t) {
+    if constexpr (OPB == 4)
+        if (t.m == 32 && t.n == 32) return TileCfg<32, 32, 4>::RB;
     if (t.m == 64 && t.n == 64) return TileCfg<64, 64, OPB>::RB;
     if (t.m == 64 && t.n == 128) return TileCfg<64, 128, OPB>::RB;
     if (t.m == 64 && t.n == 256) return TileCfg<64, 256, OPB>::RB;
@@ -529,7 +541,7 @@ int ensure_workspace(pcd_model* m, hipStream_t stream, int rows, Workspace** out
     if ((st = dev_alloc_zero(w->owned, (void**)&w->split_part, (size_t)split_part_tiles(m) * 128 * 128 * 4)))
         return st;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->split_count, split_count_bytes(m)))) return st;
-    if ((st = dev_alloc_zero(w->owned, (void**)&w->act_tm, (size_t)(need / 64) * 4))) return st;
+    if ((st = dev_alloc_zero(w->owned, (void**)&w->act_tm, (size_t)(need / kMinTileM) * 4))) return st;
     if ((st = dev_alloc_zero(w->owned, (void**)&w->act_count, 4))) return st;
     if ((st = dev_alloc_zero(w->owned, &w->persist, kPersistBytes))) return st;
     HIP_TRY(hipStreamCreateWithFlags(&w->capture, hipStreamNonBlocking));
@@ -1521,11 +1533,11 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
     std::string n(name);
     if (n == "use_graph") m->use_graph = value ? 1 : 0;
     else if (n == "tile") {
-        if (value != 0 && !tile_supported(Tile{value, value}))
-            return fail(PCD_INVALID_VALUE, "tile must be 0, 64, 128 or 256");
+        if (value != 0 && !tile_supported(Tile{value, value}, m->dtype))
+            return fail(PCD_INVALID_VALUE, "tile must be 0, 64, 128 or 256 (or 32 on fp32 models)");
         m->tile_m = m->tile_n = value;
     } else if (n == "tile_n") {
-        if (m->tile_m == 0 || !tile_supported(Tile{m->tile_m, value}))
+        if (m->tile_m == 0 || !tile_supported(Tile{m->tile_m, value}, m->dtype))
             return fail(PCD_INVALID_VALUE, "tile_n: unsupported tile %d x %d (set tile first)", m->tile_m, value);
         m->tile_n = value;
     } else if (n == "profile") m->profile = value ? 1 : 0;

@@ -33,6 +33,7 @@ int persistent_blocks_per_cu();
     PCD_DECLARE_TILE(OP, 256, 128) \
     PCD_DECLARE_TILE(OP, 256, 256)
 PCD_DECLARE_OP(float)
+PCD_DECLARE_TILE(float, 32, 32)
 PCD_DECLARE_OP(bf16_t)
 PCD_DECLARE_OP(f16_t)
 #undef PCD_DECLARE_OP

@@ -57,7 +57,7 @@ def test_classify_adaptive_fp32_matches_oracle(oracle, act, ffg):
         m.close()
 
 
-@pytest.mark.parametrize("tile", [0, 64, 128])
+@pytest.mark.parametrize("tile", [0, 32, 64, 128])
 def test_classify_adaptive_c1_network(oracle, tile):
     # c1's network (784-256-256-10 tanh) with a batch of 24 samples: 240
     # one-row candidates, each with its own exit step

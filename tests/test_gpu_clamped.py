@@ -73,7 +73,7 @@ def test_clamped_two_level_network_energy_only(oracle):
     assert max_rel(en, ren) < 1e-4
 
 
-@pytest.mark.parametrize("tile", [0, 64, 128, 256])
+@pytest.mark.parametrize("tile", [0, 32, 64, 128, 256])
 def test_classify_c1_shape_fp32(oracle, tile):
     # the reference's MNIST-shaped classifier ([784,256,256,10] tanh) on a batch of 24
     snap, W, b, P, x = build_case([784, 256, 256, 10], "tanh", 0.1, batch=24, xdist="uniform01", seed=0)
