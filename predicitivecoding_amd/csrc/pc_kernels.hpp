@@ -488,6 +488,163 @@ template <typename OP> struct PackOp {
 
 typedef const __attribute__((address_space(4))) Problem KProblem;
 
+// The end of a settling phase unit on the K-shared 32 x 32 tile (fp32).  On
+// entry each of the 4 waves holds its partial sum of the whole block over its
+// quarter of K (`acc`, transposed layout: lane l has row l % 32, register
+// 4g + k is column 8g + 4(l / 32) + k).  Reduce-scatter through LDS: wave w
+// ends with group w (columns 8w + 4(l / 32) .. +3 of its row) summed over the
+// waves in wave order; then split-K, if any, per group; then the error or
+// update epilogue per group, so each wave evaluates a quarter of the block's
+// activations and stores its 16 bytes per row directly.  The error phase's
+// row energies meet across the groups through LDS, in group order.
+template <int BM, int BN, int EPI>
+__device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArgs& args, const f32x16& acc, char* smem,
+                                                const int tile, const int split, const int ks, const int row0,
+                                                const int col0, const int tn) {
+    using C = TileCfg<BM, BN, 4>;
+    static_assert(C::KW == 4 && C::FM == 1 && C::FN == 1, "one block shared by four waves");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, half = lane >> 5;
+    float* red = (float*)smem;                                   // 4 waves x 16 registers x 64 lanes
+    float* ered = (float*)(smem + C::KW * 16 * 64 * 4);          // 4 groups x 32 rows
+    __syncthreads();   // every wave is done reading the stage ring
+    static_for<0, 16>([&](auto R) PCD_INLINE {
+        constexpr int r = decltype(R)::value;
+        red[(wave * 16 + r) * 64 + lane] = acc[r];
+    });
+    __syncthreads();
+    f32x4 g;
+    static_for<0, 4>([&](auto K) PCD_INLINE {
+        constexpr int k = decltype(K)::value;
+        float v = red[(4 * wave + k) * 64 + lane];
+        static_for<1, C::KW>([&](auto W) PCD_INLINE { v += red[(decltype(W)::value * 16 + 4 * wave + k) * 64 + lane]; });
+        g[k] = v;
+    });
+
+    if (ks > 1) {
+        // Split-K per group, the handshake of the other tiles (see phase_unit):
+        // each wave publishes its group's two 64-bit words per lane; the range
+        // that finishes last sums every range's group in range order.
+        typedef unsigned long long u64;
+        u64* part = (u64*)(P.part + (size_t)tile * ks * (BM * BN));
+        constexpr int UNIT = BM * BN / 2;
+        const int slot = (wave * 64 + lane) * 2;
+        auto pack = [](float a, float b) PCD_INLINE { return (u64)__float_as_uint(a) | ((u64)__float_as_uint(b) << 32); };
+        __hip_atomic_store(part + (size_t)split * UNIT + slot, pack(g[0], g[1]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part + (size_t)split * UNIT + slot + 1, pack(g[2], g[3]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        wait_vmcnt<0>();
+        __syncthreads();
+        int* flag = (int*)(ered + C::KW * 32);
+        if (tid == 0) *flag = __hip_atomic_fetch_add(P.count + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*flag != ks - 1) return;
+        if (tid == 0) __hip_atomic_store(P.count + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+        u64 pv[kMaxSplit][2];
+        static_for<0, kMaxSplit>([&](auto Kc) PCD_INLINE {
+            constexpr int k = decltype(Kc)::value;
+            if (k < ks && k != split)
+                static_for<0, 2>([&](auto Q) PCD_INLINE {
+                    pv[k][decltype(Q)::value] = __hip_atomic_load(part + (size_t)k * UNIT + slot + decltype(Q)::value,
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                });
+        });
+        f32x4 sum{};
+        static_for<0, kMaxSplit>([&](auto Kc) PCD_INLINE {
+            constexpr int k = decltype(Kc)::value;
+            if (k < ks) {
+                f32x4 v = g;
+                if (k != split)
+                    v = f32x4{__uint_as_float((uint32_t)pv[k][0]), __uint_as_float((uint32_t)(pv[k][0] >> 32)),
+                              __uint_as_float((uint32_t)pv[k][1]), __uint_as_float((uint32_t)(pv[k][1] >> 32))};
+                sum = k == 0 ? v : sum + v;
+            }
+        });
+        g = sum;
+    }
+
+    // Row lr of the block, columns col .. col + 3.  The operands are read
+    // whatever the row's state (rows and columns are padded in memory, the
+    // padding is zero); only valid rows and columns below N are written.
+    const int row = row0 + lr, col = col0 + 8 * wave + 4 * half;
+    const bool rok = row < P.M && row_active(args, row);
+    const bool cfull = col + 3 < P.N;
+    const size_t idx = (size_t)row * P.ldo + col;
+    auto store4 = [&](float* dst, const f32x4& v) PCD_INLINE {
+        if (!rok) return;
+        if (cfull) {
+            gst4(dst + idx, v);
+        } else {
+            static_for<0, 4>([&](auto K) PCD_INLINE {
+                constexpr int k = decltype(K)::value;
+                if (col + k < P.N) gst(dst + idx + k, v[k]);
+            });
+        }
+    };
+    if constexpr (EPI == EPI_ERROR) {
+        const f32x4 mv = gld4(P.mlow + idx);
+        const f32x4 bv = gld4(P.bias + col);
+        const float P_low = P.prec, inv2p = 0.5f / P.prec, eta = args.eta, lam = args.act_reg;
+        f32x4 dv, xv;
+        float es = 0.f;
+        auto body = [&](auto ActC) PCD_INLINE {
+            constexpr int ACT = decltype(ActC)::value;
+            static_for<0, 4>([&](auto K) PCD_INLINE {
+                constexpr int k = decltype(K)::value;
+                float y, dy;
+                act_eval(ACT, g[k] + bv[k], y, dy);
+                const float m = mv[k];
+                const float e = P_low * (m - y);
+                dv[k] = dy * e;
+                // X = M - eta (e + lambda sign M): the state's own part of its update
+                float gr = e;
+                if (lam > 0.f) gr += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
+                xv[k] = m - eta * gr;
+                if (rok && col + k < P.N) es += e * e;
+            });
+        };
+        switch (args.act) {
+        case ACT_TANH: body(std::integral_constant<int, ACT_TANH>{}); break;
+        case ACT_RELU: body(std::integral_constant<int, ACT_RELU>{}); break;
+        case ACT_SIGMOID: body(std::integral_constant<int, ACT_SIGMOID>{}); break;
+        case ACT_GELU: body(std::integral_constant<int, ACT_GELU>{}); break;
+        default: body(std::integral_constant<int, ACT_LINEAR>{}); break;
+        }
+        if (P.eout) store4(P.eout, xv);
+        store4((float*)P.dout, dv);
+        if (args.energy_part != nullptr) {
+            // this group's 8 columns of the row (both half-waves), then the
+            // four groups in order
+            float v = es * inv2p;
+            v += __shfl_xor(v, 32);
+            if (half == 0) ered[wave * 32 + lr] = v;
+            __syncthreads();
+            if (wave == 0 && half == 0 && row < P.M) {
+                const float e4 = ((ered[lr] + ered[32 + lr]) + ered[64 + lr]) + ered[96 + lr];
+                gst(args.energy_part + (size_t)(P.slot_base + tn * C::WN) * args.ldp + row, e4);
+            }
+        }
+    } else {
+        // M_l = X_l + eta G below the top (X_l written by the error phase); the
+        // top layer reads M_l itself: M_l -= eta (lambda sign M_l - G).
+        const float eta = args.eta, lam = args.act_reg;
+        const bool folded = P.eself != nullptr;
+        const f32x4 xv = gld4((folded ? P.eself : P.m) + idx);
+        f32x4 mn;
+        static_for<0, 4>([&](auto K) PCD_INLINE {
+            constexpr int k = decltype(K)::value;
+            if (folded) {
+                mn[k] = xv[k] + eta * g[k];
+            } else {
+                float grad = -g[k];
+                if (lam > 0.f) grad += lam * (xv[k] > 0.f ? 1.f : (xv[k] < 0.f ? -1.f : 0.f));
+                mn[k] = xv[k] - eta * grad;
+            }
+        });
+        store4(P.m, mn);
+    }
+}
+
 // LDS of one phase unit: the stage ring, which after the main loop the
 // settling epilogues reuse as two store-staging regions per wave and the
 // tile's bias.
@@ -671,12 +828,11 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             b[j] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
         }
     };
-    // The settling epilogues take each block transposed (TR): the B-side
-    // fragment goes in as the MFMA's first operand, so a lane holds one row
-    // and runs of four consecutive columns (the result layout at the top of
-    // this file with rows and columns exchanged), which those epilogues read
-    // and write 16 bytes at a time.
-    constexpr bool TR = EPI == EPI_ERROR || EPI == EPI_UPDATE;
+    // The settling epilogues (error, update) take each block transposed: the
+    // B-side fragment goes in as the MFMA's first operand, so a lane holds one
+    // row and runs of four consecutive columns, which those epilogues read and
+    // write 16 bytes at a time.
+    constexpr bool TRM = EPI == EPI_ERROR || EPI == EPI_UPDATE;
     auto mfmas = [&](const u32x4* a, const u32x4* b) PCD_INLINE {
         if constexpr (F32OP) {
             // K component s of every block before component s + 1 of any.
@@ -686,8 +842,8 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
                     static_for<0, C::FN>([&](auto J) PCD_INLINE {
                         constexpr int i = decltype(I)::value, j = decltype(J)::value;
                         const float av = __uint_as_float(a[i][s]), bv = __uint_as_float(b[j][s]);
-                        accs[k][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(TR ? bv : av, TR ? av : bv, accs[k][i][j],
-                                                                            0, 0, 0);
+                        accs[k][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(TRM ? bv : av, TRM ? av : bv,
+                                                                            accs[k][i][j], 0, 0, 0);
                     });
                 });
             });
@@ -695,7 +851,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             static_for<0, C::FM>([&](auto I) PCD_INLINE {
                 static_for<0, C::FN>([&](auto J) PCD_INLINE {
                     constexpr int i = decltype(I)::value, j = decltype(J)::value;
-                    if constexpr (TR) mfma_chunk<OP>(accs[0][i][j], b[j], a[i]);
+                    if constexpr (TRM) mfma_chunk<OP>(accs[0][i][j], b[j], a[i]);
                     else mfma_chunk<OP>(accs[0][i][j], a[i], b[j]);
                 });
             });
@@ -759,6 +915,15 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             for (int j = 0; j < C::FN; ++j) accs[0][i][j] += accs[decltype(Kc)::value][i][j];
     });
     f32x16 (&acc)[C::FM][C::FN] = accs[0];
+    // The settling epilogues take each block transposed (TR): the B-side
+    // fragment went in as the MFMA's first operand, so a lane holds one row
+    // and runs of four consecutive columns (the result layout at the top of
+    // this file with rows and columns exchanged).
+    constexpr bool TR = EPI == EPI_ERROR || EPI == EPI_UPDATE;
+    if constexpr (C::KW > 1 && TR) {
+        ksw_settle_tail<BM, BN, EPI>(P, args, acc[0][0], smem, local, split, ks, row0, col0, tn);
+        return;
+    }
     if constexpr (C::KW > 1) {
         // The waves' partial sums of the block meet in LDS (lane-contiguous,
         // conflict-free); every wave adds them in wave order, so all of them
