@@ -386,7 +386,8 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *   profile      while set, pcd_pc_relax and pcd_pc_relax_ragged run eagerly and
  *                time every phase launch with HIP events (pcd_pc_profile_result)
  *   split_min    fewest K stages a split-K range of a settling phase takes
- *                (default 12; fewer gives more, shorter ranges)
+ *                (0, the default: 4 on the 32 x 32 tile, 12 on the others;
+ *                fewer gives more, shorter ranges)
  *   persistent   1: a fixed-step fp32 settling whose phases deal at most two
  *                workgroups per CU (64 x 64 tiles, at most 6 problems a phase)
  *                runs as one cooperative launch of the whole step loop, with

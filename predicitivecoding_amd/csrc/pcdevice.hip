@@ -253,6 +253,10 @@ constexpr int kMaxKStagger = 64;
 #define PCD_SPLIT_MIN_STAGES 12
 #endif
 constexpr int kSplitMinStages = PCD_SPLIT_MIN_STAGES;
+// The same on the K-shared 32 x 32 tile, whose ranges publish and sum a
+// quarter of a block per wave (784-256-256-10 at a batch of 64: 4 beats 12
+// by 6%, 2 loses 5%).
+constexpr int kSplitMinStagesKsw = 4;
 // Persistent settling buffer: the grid barrier's arrival count and give-up flag.
 constexpr size_t kPersistBytes = 256;
 constexpr int kPersistSpinDefault = 1 << 22;   // about a second of polls (each a device-scope load and a sleep)
@@ -322,7 +326,7 @@ struct pcd_model {
     // options
     int use_graph = 1, tile_m = 0, tile_n = 0, profile = 0, tile_order = TILE_INTERLEAVED, split_k = 1;
     int persistent = 0;                 // fixed-step fp32 settlings of few tiles as one persistent launch (opt-in)
-    int split_min = kSplitMinStages;    // fewest K stages of a split-K range in the settling phases
+    int split_min = 0;                  // fewest K stages of a split-K range in the settling phases (0: by tile)
     int persist_spin = kPersistSpinDefault;
     int persist_grid = 0;               // workgroups of the persistent launch (0: automatic)
     int k_stagger = 0;                  // settling phases: kKStaggerAuto (16-bit default), 0 off, or a fixed value
@@ -613,8 +617,9 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
     sc.part = w->split_part;
     sc.count = w->split_count;
     sc.budget = split_part_tiles(m);
-    assign_split(m->cus, m->split_k, m->dtype, tile, sc, err, m->split_min);
-    assign_split(m->cus, m->split_k, m->dtype, tile, sc, upd, m->split_min);
+    const int smin = m->split_min > 0 ? m->split_min : tile.m == 32 ? kSplitMinStagesKsw : kSplitMinStages;
+    assign_split(m->cus, m->split_k, m->dtype, tile, sc, err, smin);
+    assign_split(m->cus, m->split_k, m->dtype, tile, sc, upd, smin);
     *nslots = slot;
 }
 
@@ -1549,7 +1554,7 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
     } else if (n == "ragged_tiles") m->ragged_tiles = value ? 1 : 0;
     else if (n == "persistent") m->persistent = value ? 1 : 0;
     else if (n == "split_min") {
-        if (value < 1) return fail(PCD_INVALID_VALUE, "split_min must be >= 1");
+        if (value < 0) return fail(PCD_INVALID_VALUE, "split_min must be >= 0 (0: automatic)");
         m->split_min = value;
     }
     else if (n == "persist_spin") {

@@ -460,6 +460,9 @@ def test_device_errors_are_status_codes():
         assert L.pcd_pc_relax(m.handle, 1, 2, 0, 1, None, None, None) == DeviceStatus.InvalidValue
         with pytest.raises(DeviceException):
             m.set_option("tile", 96)
+        with pytest.raises(DeviceException):
+            m.set_option("split_min", -1)
+        m.set_option("split_min", 0)   # automatic
     finally:
         m.close()
 
