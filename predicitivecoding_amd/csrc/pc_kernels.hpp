@@ -339,6 +339,12 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
 #ifndef PCD_SMALL_RB16
 #define PCD_SMALL_RB16 128
 #endif
+#ifndef PCD_KSW_NS
+#define PCD_KSW_NS 3   // the K-shared 32 x 32 tile: 48 KB ring, three workgroups per CU
+#endif
+#ifndef PCD_KSW_OCC
+#define PCD_KSW_OCC 3
+#endif
 template <int BM, int BN, int OPB = 4> struct TileCfg {
     // 256 x 256 runs 8 waves (2 x 4 of 128 x 64: two waves per SIMD share the
     // MFMA pipe) over 128-byte K stages, double buffered (128 KB of LDS, one
@@ -364,10 +370,10 @@ template <int BM, int BN, int OPB = 4> struct TileCfg {
     static constexpr int NC = RB / 32;                     // 32-byte MFMA chunks per stage
     static constexpr int NCW = NC / KW;                    // chunks of a stage one wave takes
     static constexpr int stage_bytes = (BM + BN) * RB;
-    static constexpr int NS_WANT = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : (BM + BN >= 320) ? 3 : PCD_SMALL_NS;
+    static constexpr int NS_WANT = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : KSW ? PCD_KSW_NS : (BM + BN >= 320) ? 3 : PCD_SMALL_NS;
     static constexpr int NS = BIG ? NS_WANT : (NS_WANT * stage_bytes <= 80 * 1024 ? NS_WANT : 80 * 1024 / stage_bytes);   // stages in the LDS ring
     static constexpr int D = NS - 1;                       // prefetch distance (stages)
-    static constexpr int OCC = BIG ? 1 : PCD_OCC_SMALL;    // workgroups per CU the registers are sized for
+    static constexpr int OCC = BIG ? 1 : KSW ? PCD_KSW_OCC : PCD_OCC_SMALL;   // workgroups per CU the registers are sized for
     static constexpr int ROWS_PER_LOAD = 64 * 16 / RB;     // rows one wave-wide 16-byte-per-lane load fills
     static constexpr int QPW = (BM + BN) / ROWS_PER_LOAD / NWAVES;   // loads per wave per stage
     static_assert(FM >= 1 && FN >= 1 && QPW >= 1, "tile too small");
@@ -650,7 +656,9 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
 // tile's bias.
 template <typename OP, int BM, int BN> constexpr int phase_smem_bytes() {
     using C = TileCfg<BM, BN, OpTraits<OP>::bytes>;
-    constexpr int STAGE_END = 2 * C::NWAVES * kStageWaveBytes + BN * 4;
+    // The K-shared tile's tail needs its reduce-scatter, the row energies and a
+    // flag; the others two store-staging regions per wave and the bias.
+    constexpr int STAGE_END = C::KSW ? C::KW * 16 * 64 * 4 + C::KW * 32 * 4 + 16 : 2 * C::NWAVES * kStageWaveBytes + BN * 4;
     return C::NS * C::stage_bytes > STAGE_END ? C::NS * C::stage_bytes : STAGE_END;
 }
 

@@ -194,6 +194,17 @@ def test_rows_are_independent_bit_for_bit():
     assert np.array_equal(one[0], top[17])
 
 
+@pytest.mark.parametrize("tile", [32, 64])
+def test_fixed_tile_without_split_k_makes_rows_independent_of_batch_size(tile):
+    # with the tile forced and split-K off, a row sums K in the same order
+    # whatever the batch size (the automatic tile and split follow it)
+    snap, W, b, P, x = build_case([300, 520, 130, 24], "gelu", 0.1, batch=700, seed=17, init="fanin")
+    opts = {"tile": tile, "split_k": 0}
+    big, _, ebig = run_gpu(snap, x, 6, energy=True, options=opts)
+    small, _, esmall = run_gpu(snap, x[40:45], 6, energy=True, options=opts)
+    assert np.array_equal(big[40:45], small) and np.array_equal(ebig[:, 40:45], esmall)
+
+
 def test_two_level_network():
     # L = 2: a single weight matrix, top is the only free layer
     from tests.netgen import make_inputs
