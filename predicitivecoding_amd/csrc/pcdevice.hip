@@ -1203,11 +1203,14 @@ int pcd_event_elapsed_ms(float* ms, void* start, void* end) {
 
 // Output tile of a provider GEMM: 256 x 256 (16-bit operands) while it still
 // gives every CU a tile, then 128 x 128 while that does, else 64 x 64 (whose
-// few tiles split-K then spreads over the CUs).
-static Tile choose_gemm_tile(int dtype, int m, int n, int cus) {
-    auto tiles = [&](int t) { return (long)((m + t - 1) / t) * ((n + t - 1) / t); };
+// few tiles split-K then spreads over the CUs); fp32 products with fewer
+// 64 x 64 tiles than CUs take the K-shared 32 x 32 tile.  `batch` products of
+// the same shape count together.
+static Tile choose_gemm_tile(int dtype, int m, int n, int cus, int batch = 1) {
+    auto tiles = [&](int t) { return (long)batch * ((m + t - 1) / t) * ((n + t - 1) / t); };
     if (dtype != PCD_F32 && tiles(256) >= cus) return Tile{256, 256};
     if (tiles(128) >= cus) return Tile{128, 128};
+    if (dtype == PCD_F32 && tiles(64) < cus) return Tile{32, 32};
     return Tile{64, 64};
 }
 
@@ -1282,7 +1285,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
             st = launch_zero(sc.count, cnt_bytes, s);
         }
     }
-    if (!st) assign_split(cus, 1, dtype, tile, sc, sets);
+    if (!st) assign_split(cus, 1, dtype, tile, sc, sets, tile.m == 32 ? kSplitMinStagesKsw : kSplitMinStages);
     PhaseArgs a;
     std::memset(&a, 0, sizeof a);
     a.alpha = 1.f;
@@ -1311,10 +1314,7 @@ static int gemm_batched_common(int dtype, const void* dA, const void* dB, float*
     int dev = 0, cus = 256;
     HIP_TRY(hipGetDevice(&dev));
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    auto tiles = [&](int t) { return (long)batch * ((m + t - 1) / t) * ((n + t - 1) / t); };
-    const Tile tile = (dtype != PCD_F32 && tiles(256) >= cus) ? Tile{256, 256}
-                      : tiles(128) >= cus                     ? Tile{128, 128}
-                                                              : Tile{64, 64};
+    const Tile tile = choose_gemm_tile(dtype, m, n, cus, batch);
     const int mp = (int)round_up(m, tile.m), np = (int)round_up(n, tile.n), kp = (int)round_up(k, kFeatPad);
     const int ob = op_bytes(dtype);
     const size_t a_item = (size_t)mp * kp * ob, b_item = (size_t)np * kp * ob;
