@@ -356,11 +356,10 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *                for pcd_pc_relax_ragged also requests, exit rule, threshold)
  *   tile, tile_n force a GEMM tile (0 = automatic choice): tile sets rows and
  *                columns, tile_n then the columns; supported 64 x 64,
- *                64 x 128, 64 x 256, 128 x 128, 256 x 128, 256 x 256, and
- *                on fp32 models 32 x 32 (the four waves of a workgroup share
- *                the tile's K; the automatic choice for an fp32 settling with
- *                fewer 64 x 64 error-phase tiles than CUs, unless
- *                `persistent` is on)
+ *                64 x 128, 64 x 256, 128 x 128, 256 x 128, 256 x 256 and
+ *                32 x 32 (the four waves of a workgroup share the tile's K;
+ *                the automatic choice for a settling with fewer 64 x 64
+ *                error-phase tiles than CUs, unless `persistent` is on)
  *   tile_order   0: every XCD runs an eighth of each problem's tiles (default);
  *                1: every XCD runs one contiguous eighth of the phase's tiles
  *   split_k      1: phases with fewer tiles than half the CUs split K over

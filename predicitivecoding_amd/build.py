@@ -20,8 +20,7 @@ HOST_SOURCE = os.path.join(CSRC, "pcdevice.hip")
 INST_SOURCE = os.path.join(CSRC, "phase_inst.hip")
 
 OPS = {"f32": 0, "bf16": 1, "f16": 2}
-TILES = [(64, 64), (64, 128), (64, 256), (128, 128), (256, 128), (256, 256)]
-TILES_F32 = [(32, 32)]   # the K-shared tile, fp32 operands only
+TILES = [(32, 32), (64, 64), (64, 128), (64, 256), (128, 128), (256, 128), (256, 256)]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -35,7 +34,7 @@ def _units():
     """(source, extra flags, object name) of every translation unit."""
     units = [(HOST_SOURCE, [], "pcdevice.o")]
     for op, op_id in OPS.items():
-        for bm, bn in TILES + (TILES_F32 if op == "f32" else []):
+        for bm, bn in TILES:
             units.append((INST_SOURCE, [f"-DPCD_OP_ID={op_id}", f"-DPCD_BM={bm}", f"-DPCD_BN={bn}"],
                           f"phase_{op}_{bm}x{bn}.o"))
     return units

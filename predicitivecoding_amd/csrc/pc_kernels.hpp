@@ -354,10 +354,11 @@ template <int BM, int BN, int OPB = 4> struct TileCfg {
     // line of every weight row per stage, which is what streams best from HBM
     // when the batch is small (the weights dominate the traffic).
     static constexpr bool BIG = BM == 256 && BN == 256;
-    // 32 x 32 (fp32 only) is one output block whose K the 4 waves share: each
-    // stage holds 64 K elements per row and wave w takes the w-th quarter of
-    // every stage, so a tile's K sweep takes a quarter of the MFMA issue time
-    // of a 64 x 64 tile's.  The waves' sums meet in LDS after the loop.
+    // 32 x 32 is one output block whose K the 4 waves share: each stage holds
+    // 64 K elements per row (256 bytes of fp32, 128 of 16-bit operands) and
+    // wave w takes the w-th quarter of every stage, so a tile's K sweep takes
+    // a quarter of the MFMA issue time of a 64 x 64 tile's.  The waves' sums
+    // meet in LDS after the loop.
     static constexpr bool KSW = BM == 32 && BN == 32;
     static constexpr int KW = KSW ? 4 : 1;                 // waves sharing one block's K
     static constexpr int WM = KSW ? 1 : 2, WN = BIG ? 4 : KSW ? 1 : 2;
@@ -365,7 +366,7 @@ template <int BM, int BN, int OPB = 4> struct TileCfg {
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
     static constexpr bool MID = BM == 128 && BN == 128;
-    static constexpr int RB = BIG ? PCD_BIG_RB : MID ? PCD_MID_RB : KSW ? 256 : (BM == 64 && OPB == 2) ? PCD_SMALL_RB16 : PCD_SMALL_RB;   // K bytes per row per stage
+    static constexpr int RB = BIG ? PCD_BIG_RB : MID ? PCD_MID_RB : KSW ? 64 * OPB : (BM == 64 && OPB == 2) ? PCD_SMALL_RB16 : PCD_SMALL_RB;   // K bytes per row per stage
     static constexpr int UNITS = RB / 16;                  // 16-byte units per row
     static constexpr int NC = RB / 32;                     // 32-byte MFMA chunks per stage
     static constexpr int NCW = NC / KW;                    // chunks of a stage one wave takes
@@ -378,8 +379,7 @@ template <int BM, int BN, int OPB = 4> struct TileCfg {
     static constexpr int QPW = (BM + BN) / ROWS_PER_LOAD / NWAVES;   // loads per wave per stage
     static_assert(FM >= 1 && FN >= 1 && QPW >= 1, "tile too small");
     static_assert((BM + BN) % (NWAVES * ROWS_PER_LOAD) == 0, "stage rows must split evenly over the waves");
-    static_assert(NCW % 2 == 0, "fragment buffers alternate within a stage");
-    static_assert(!KSW || OPB == 4, "the 32 x 32 tile takes fp32 operands");
+    static_assert(NCW % 2 == 0 || NCW == 1, "fragment buffers alternate within a stage (or per stage)");
     static_assert(D >= 1 && D * QPW < 64, "stage_ready waits on at most 63 loads");
     static_assert(NS * stage_bytes <= 160 * 1024, "LDS ring exceeds the 160 KB of a CU");
     static_assert(64 % (RB / OPB) == 0, "K is padded to 64 elements: a stage's K must divide it");
@@ -494,20 +494,21 @@ template <typename OP> struct PackOp {
 
 typedef const __attribute__((address_space(4))) Problem KProblem;
 
-// The end of a settling phase unit on the K-shared 32 x 32 tile (fp32).  On
+// The end of a settling phase unit on the K-shared 32 x 32 tile.  On
 // entry each of the 4 waves holds its partial sum of the whole block over its
 // quarter of K (`acc`, transposed layout: lane l has row l % 32, register
 // 4g + k is column 8g + 4(l / 32) + k).  Reduce-scatter through LDS: wave w
 // ends with group w (columns 8w + 4(l / 32) .. +3 of its row) summed over the
 // waves in wave order; then split-K, if any, per group; then the error or
 // update epilogue per group, so each wave evaluates a quarter of the block's
-// activations and stores its 16 bytes per row directly.  The error phase's
+// activations and stores its four columns per row directly (fp32 states,
+// operand-type deltas and state copies).  The error phase's
 // row energies meet across the groups through LDS, in group order.
-template <int BM, int BN, int EPI>
+template <typename OP, int BM, int BN, int EPI>
 __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArgs& args, const f32x16& acc, char* smem,
                                                 const int tile, const int split, const int ks, const int row0,
                                                 const int col0, const int tn) {
-    using C = TileCfg<BM, BN, 4>;
+    using C = TileCfg<BM, BN, OpTraits<OP>::bytes>;
     static_assert(C::KW == 4 && C::FM == 1 && C::FN == 1, "one block shared by four waves");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, half = lane >> 5;
     float* red = (float*)smem;                                   // 4 waves x 16 registers x 64 lanes
@@ -576,6 +577,8 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
     const bool rok = row < P.M && row_active(args, row);
     const bool cfull = col + 3 < P.N;
     const size_t idx = (size_t)row * P.ldo + col;
+    // fp32 (`store4`) and operand-type (`store4_op`) stores of this lane's four
+    // columns.
     auto store4 = [&](float* dst, const f32x4& v) PCD_INLINE {
         if (!rok) return;
         if (cfull) {
@@ -584,6 +587,17 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
             static_for<0, 4>([&](auto K) PCD_INLINE {
                 constexpr int k = decltype(K)::value;
                 if (col + k < P.N) gst(dst + idx + k, v[k]);
+            });
+        }
+    };
+    auto store4_op = [&](void* dst, const f32x4& v) PCD_INLINE {
+        if (!rok) return;
+        if (cfull) {
+            OpTraits<OP>::store4(dst, idx, v);
+        } else {
+            static_for<0, 4>([&](auto K) PCD_INLINE {
+                constexpr int k = decltype(K)::value;
+                if (col + k < P.N) OpTraits<OP>::store(dst, idx + k, v[k]);
             });
         }
     };
@@ -617,7 +631,7 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
         default: body(std::integral_constant<int, ACT_LINEAR>{}); break;
         }
         if (P.eout) store4(P.eout, xv);
-        store4((float*)P.dout, dv);
+        store4_op(P.dout, dv);
         if (args.energy_part != nullptr) {
             // this group's 8 columns of the row (both half-waves), then the
             // four groups in order
@@ -648,6 +662,7 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
             }
         });
         store4(P.m, mn);
+        if (P.mop) store4_op(P.mop, mn);
     }
 }
 
@@ -899,17 +914,26 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // first fragments it overlaps.  The last stage is peeled off.
     for (int kt = 0; kt + 1 < nk; ++kt) {
         if (kt + C::D < nk) issue_stage(kt + C::D);
-        static_for<0, NC>([&](auto Cc) PCD_INLINE {
-            constexpr int c = decltype(Cc)::value;
-            if constexpr (c + 1 < NC) {
-                read_frags(kt % C::NS, c0 + c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
-            } else {
-                stage_ready(kt + 1);
-                read_frags((kt + 1) % C::NS, c0, fa[0], fb[0]);
-            }
-            mfmas(fa[c & 1], fb[c & 1]);
-            interleave();
-        });
+        if constexpr (NC == 1) {
+            // One chunk per wave and stage (the K-shared tile on 16-bit
+            // operands): its MFMA runs across the barrier, and the next
+            // stage's fragments are read into the same registers after it.
+            mfmas(fa[0], fb[0]);
+            stage_ready(kt + 1);
+            read_frags((kt + 1) % C::NS, c0, fa[0], fb[0]);
+        } else {
+            static_for<0, NC>([&](auto Cc) PCD_INLINE {
+                constexpr int c = decltype(Cc)::value;
+                if constexpr (c + 1 < NC) {
+                    read_frags(kt % C::NS, c0 + c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
+                } else {
+                    stage_ready(kt + 1);
+                    read_frags((kt + 1) % C::NS, c0, fa[0], fb[0]);
+                }
+                mfmas(fa[c & 1], fb[c & 1]);
+                interleave();
+            });
+        }
     }
     static_for<0, NC>([&](auto Cc) PCD_INLINE {
         constexpr int c = decltype(Cc)::value;
@@ -929,7 +953,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // this file with rows and columns exchanged).
     constexpr bool TR = EPI == EPI_ERROR || EPI == EPI_UPDATE;
     if constexpr (C::KW > 1 && TR) {
-        ksw_settle_tail<BM, BN, EPI>(P, args, acc[0][0], smem, local, split, ks, row0, col0, tn);
+        ksw_settle_tail<OP, BM, BN, EPI>(P, args, acc[0][0], smem, local, split, ks, row0, col0, tn);
         return;
     }
     if constexpr (C::KW > 1) {

@@ -168,15 +168,14 @@ int launch_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid,
 struct Tile {
     int m, n;
 };
-bool tile_supported(Tile t, int dtype) {
-    return (t.m == 32 && t.n == 32 && dtype == PCD_F32) || (t.m == 64 && (t.n == 64 || t.n == 128 || t.n == 256)) ||
+bool tile_supported(Tile t) {
+    return (t.m == 32 && t.n == 32) || (t.m == 64 && (t.n == 64 || t.n == 128 || t.n == 256)) ||
            (t.m == 128 && t.n == 128) || (t.m == 256 && t.n == 128) || (t.m == 256 && t.n == 256);
 }
 
 template <typename OP>
 int launch_op(Tile tile, int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
-    if constexpr (std::is_same<OP, float>::value)
-        if (tile.m == 32 && tile.n == 32) return launch_tile<OP, 32, 32>(epi, set, args, grid, s);
+    if (tile.m == 32 && tile.n == 32) return launch_tile<OP, 32, 32>(epi, set, args, grid, s);
     if (tile.m == 64 && tile.n == 64) return launch_tile<OP, 64, 64>(epi, set, args, grid, s);
     if (tile.m == 64 && tile.n == 128) return launch_tile<OP, 64, 128>(epi, set, args, grid, s);
     if (tile.m == 64 && tile.n == 256) return launch_tile<OP, 64, 256>(epi, set, args, grid, s);
@@ -369,14 +368,15 @@ long error_phase_tiles(const pcd_model* m, int batch, Tile t) {
 // The largest tile that still gives every CU at least two workgroups per
 // phase (a phase with fewer tiles leaves SIMDs idle: 64 x 64 beats 128 x 128
 // by 8% on the 1024-wide fp32 configuration).  256 x 256 only for 16-bit
-// operands with every layer at least 1024 wide.  An fp32 settling whose
-// error phase has fewer 64 x 64 tiles than the GPU has CUs takes the K-shared
+// operands with every layer at least 1024 wide.  A settling whose error
+// phase has fewer 64 x 64 tiles than the GPU has CUs takes the K-shared
 // 32 x 32 tile: its phases are bound by one tile's K sweep, which that tile
-// runs four times as fast (784-256-256-10 at a batch of 64: +43%), unless the
-// persistent form, built on 64 x 64, is asked for.
+// runs four times as fast, and by the epilogue, which it splits over the
+// waves (784-256-256-10 at a batch of 64: fp32 +88%, bf16 +34%), unless the
+// fp32 persistent form, built on 64 x 64, is asked for.
 Tile choose_tile(const pcd_model* m, int batch) {
     if (m->tile_m > 0) return Tile{m->tile_m, m->tile_n};
-    if (m->dtype == PCD_F32 && !m->persistent && error_phase_tiles(m, batch, Tile{64, 64}) < m->cus)
+    if (!(m->dtype == PCD_F32 && m->persistent) && error_phase_tiles(m, batch, Tile{64, 64}) < m->cus)
         return Tile{32, 32};
     // A batch that fits one 64-row tile: any taller tile is mostly padding rows
     // (its MFMAs and its state loads wasted), and the phases stream weights.
@@ -435,8 +435,7 @@ int split_factor(int cus, int split_k, long tiles, Tile tile) {
 
 // K elements of one LDS stage of `tile` for an operand type.
 template <int OPB> int stage_rb(Tile t) {
-    if constexpr (OPB == 4)
-        if (t.m == 32 && t.n == 32) return TileCfg<32, 32, 4>::RB;
+    if (t.m == 32 && t.n == 32) return TileCfg<32, 32, OPB>::RB;
     if (t.m == 64 && t.n == 64) return TileCfg<64, 64, OPB>::RB;
     if (t.m == 64 && t.n == 128) return TileCfg<64, 128, OPB>::RB;
     if (t.m == 64 && t.n == 256) return TileCfg<64, 256, OPB>::RB;
@@ -1538,11 +1537,11 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
     std::string n(name);
     if (n == "use_graph") m->use_graph = value ? 1 : 0;
     else if (n == "tile") {
-        if (value != 0 && !tile_supported(Tile{value, value}, m->dtype))
-            return fail(PCD_INVALID_VALUE, "tile must be 0, 64, 128 or 256 (or 32 on fp32 models)");
+        if (value != 0 && !tile_supported(Tile{value, value}))
+            return fail(PCD_INVALID_VALUE, "tile must be 0, 32, 64, 128 or 256");
         m->tile_m = m->tile_n = value;
     } else if (n == "tile_n") {
-        if (m->tile_m == 0 || !tile_supported(Tile{m->tile_m, value}, m->dtype))
+        if (m->tile_m == 0 || !tile_supported(Tile{m->tile_m, value}))
             return fail(PCD_INVALID_VALUE, "tile_n: unsupported tile %d x %d (set tile first)", m->tile_m, value);
         m->tile_n = value;
     } else if (n == "profile") m->profile = value ? 1 : 0;

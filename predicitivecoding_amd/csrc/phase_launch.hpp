@@ -28,12 +28,12 @@ int persistent_blocks_per_cu();
     extern template hipError_t launch_phase_tile<OP, BM, BN>(int, const ProblemSet&, const PhaseArgs&, int, \
                                                              hipStream_t);
 #define PCD_DECLARE_OP(OP)         \
+    PCD_DECLARE_TILE(OP, 32, 32)   \
     PCD_DECLARE_TILE(OP, 64, 64)   \
     PCD_DECLARE_TILE(OP, 128, 128) \
     PCD_DECLARE_TILE(OP, 256, 128) \
     PCD_DECLARE_TILE(OP, 256, 256)
 PCD_DECLARE_OP(float)
-PCD_DECLARE_TILE(float, 32, 32)
 PCD_DECLARE_OP(bf16_t)
 PCD_DECLARE_OP(f16_t)
 #undef PCD_DECLARE_OP

@@ -14,7 +14,7 @@ the oracle run with the same operand rounding.
 import numpy as np
 import pytest
 
-from predicitivecoding_amd import DeviceException, PcDeviceModel
+from predicitivecoding_amd import PcDeviceModel
 from tests.gpu_util import ACT_ID, ROUND, build_case, run_gpu, run_oracle
 from tests.netgen import make_inputs, max_rel
 
@@ -223,10 +223,6 @@ def test_relaxation_options_keep_parity(oracle, dtype, opts):
                                   bias_scale=0.1)
     m = PcDeviceModel(snap, dtype)
     try:
-        if opts.get("tile") == 32 and dtype != "f32":
-            with pytest.raises(DeviceException):   # the 32 x 32 tile takes fp32 operands only
-                m.set_option("tile", 32)
-            return
         for k, v in opts.items():
             m.set_option(k, v)
         top, st, en = m.relax(x, 7, want_states=True, want_energy=True)
