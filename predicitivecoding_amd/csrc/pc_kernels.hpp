@@ -494,16 +494,16 @@ template <typename OP> struct PackOp {
 
 typedef const __attribute__((address_space(4))) Problem KProblem;
 
-// The end of a settling phase unit on the K-shared 32 x 32 tile.  On
-// entry each of the 4 waves holds its partial sum of the whole block over its
+// The end of a settling phase unit on the K-shared 32 x 32 tile.  On entry
+// each of the 4 waves holds its partial sum of the whole block over its
 // quarter of K (`acc`, transposed layout: lane l has row l % 32, register
 // 4g + k is column 8g + 4(l / 32) + k).  Reduce-scatter through LDS: wave w
 // ends with group w (columns 8w + 4(l / 32) .. +3 of its row) summed over the
 // waves in wave order; then split-K, if any, per group; then the error or
 // update epilogue per group, so each wave evaluates a quarter of the block's
-// activations and stores its four columns per row directly (fp32 states,
-// operand-type deltas and state copies).  The error phase's
-// row energies meet across the groups through LDS, in group order.
+// activations and stores its four columns of each row directly (fp32 states,
+// operand-type deltas and state copies).  The error phase's row energies meet
+// across the groups through LDS, in group order.
 template <typename OP, int BM, int BN, int EPI>
 __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArgs& args, const f32x16& acc, char* smem,
                                                 const int tile, const int split, const int ks, const int row0,
