@@ -297,9 +297,95 @@ template <typename OP>
 __global__ void bias_update_kernel(const void* __restrict__ d, int ld, int rows, int cols, float* __restrict__ bias,
                                    float eta_w) {
     for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x) {
+        // Rows eight at a time: the loads go out together, the adds stay in
+        // row order (the same sum as one row after another).
         float s = 0.f;
-        for (int r = 0; r < rows; ++r) s += OpTraits<OP>::load(d, (size_t)r * ld + c);
+        int r = 0;
+        for (; r + 8 <= rows; r += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = OpTraits<OP>::load(d, (size_t)(r + k) * ld + c);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s += v[k];
+        }
+        for (; r < rows; ++r) s += OpTraits<OP>::load(d, (size_t)r * ld + c);
         bias[c] += eta_w * s;
+    }
+}
+
+// The learning step's weight and bias update for a small batch, every layer
+// in one launch: W_l = beta W_l + alpha D_l^T M_l (K = the batch rows, summed
+// in row order on the VALU), b_l += eta_w * (column sums of D_l, rows in
+// order), and the refreshed operand copies W_l^T and, for 16-bit models,
+// W_l, rounded as the upload rounds them.  Workgroup b runs one 32 x 32 block
+// of one layer's W (blocks counted layer after layer); lane t owns rows
+// i0 + 2 (t % 16) + {0, 1} and columns j0 + 2 (t / 16) + {0, 1}, with
+// 64-row chunks of its D and M columns staged in LDS.
+constexpr int kHebbLayers = 16;   // layers per launch
+struct HebbLayer {
+    const void* d;     // D_l [batch x ldd], operand type
+    const float* m;    // M_l [batch x ldm]
+    float* w;          // W_l, fp32 (the model's weights or 16-bit models' masters) [lo x ldw]
+    void* w16;         // 16-bit copy of W_l [lo x ldw], or null (fp32 models)
+    void* wt;          // W_l^T in the operand type [sz x ldwt]
+    float* bias;       // b_l [lo]
+    int ldd, ldm, ldw, ldwt;
+    int lo, sz;        // rows and columns of W_l
+    int blocks;        // ceil(lo / 32) * ceil(sz / 32)
+};
+struct HebbSet {
+    HebbLayer l[kHebbLayers];
+    int n, batch;
+    float alpha, beta, eta_w;
+};
+template <typename OP>
+__global__ void __launch_bounds__(256) hebbian_small_kernel(const HebbSet set) {
+    __shared__ float sd[64][33], sm[64][33];
+    int b = blockIdx.x, q = 0;
+    while (q < set.n && b >= set.l[q].blocks) b -= set.l[q++].blocks;
+    if (q >= set.n) return;
+    const HebbLayer& L = set.l[q];
+    const int nbj = (L.sz + 31) / 32;
+    const int i0 = (b / nbj) * 32, j0 = (b % nbj) * 32;
+    const int t = threadIdx.x, ti = t % 16, tj = t / 16;
+    float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}}, bs[2] = {0.f, 0.f};
+    const bool bias_lane = j0 == 0 && tj == 0;
+    for (int r0 = 0; r0 < set.batch; r0 += 64) {
+        const int nr = min(64, set.batch - r0);
+        __syncthreads();
+        for (int e = t; e < 64 * 32; e += 256) {
+            const int r = e / 32, c = e % 32;
+            const bool ok = r < nr;
+            sd[r][c] = ok && i0 + c < L.lo ? OpTraits<OP>::load(L.d, (size_t)(r0 + r) * L.ldd + i0 + c) : 0.f;
+            sm[r][c] = ok && j0 + c < L.sz ? L.m[(size_t)(r0 + r) * L.ldm + j0 + c] : 0.f;
+        }
+        __syncthreads();
+        for (int r = 0; r < nr; ++r) {
+            const float d0 = sd[r][2 * ti], d1 = sd[r][2 * ti + 1];
+            const float m0 = sm[r][2 * tj], m1 = sm[r][2 * tj + 1];
+            acc[0][0] = fmaf(d0, m0, acc[0][0]);
+            acc[0][1] = fmaf(d0, m1, acc[0][1]);
+            acc[1][0] = fmaf(d1, m0, acc[1][0]);
+            acc[1][1] = fmaf(d1, m1, acc[1][1]);
+            if (bias_lane) {
+                bs[0] += d0;
+                bs[1] += d1;
+            }
+        }
+    }
+    for (int a = 0; a < 2; ++a) {
+        const int i = i0 + 2 * ti + a;
+        if (i >= L.lo) continue;
+        if (bias_lane) L.bias[i] += set.eta_w * bs[a];
+        for (int c = 0; c < 2; ++c) {
+            const int j = j0 + 2 * tj + c;
+            if (j >= L.sz) continue;
+            float* wp = L.w + (size_t)i * L.ldw + j;
+            const float v = set.alpha * acc[a][c] + set.beta * *wp;
+            *wp = v;
+            if (L.w16) OpTraits<OP>::store(L.w16, (size_t)i * L.ldw + j, v);
+            OpTraits<OP>::store(L.wt, (size_t)j * L.ldwt + i, v);
+        }
     }
 }
 

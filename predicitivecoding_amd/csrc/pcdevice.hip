@@ -232,6 +232,11 @@ inline int op_bytes(int dtype) { return dtype == PCD_F32 ? 4 : 2; }
 constexpr int kFeatPad = 64;    // feature dims padded to the deepest LDS stage (64 elements)
 constexpr int kRowPad = 256;    // row dims padded to the widest tile
 constexpr int kMinTileM = 32;   // rows of the shortest tile
+// Learning steps of at most this many rows update the weights with
+// hebbian_small_kernel (K = rows on the VALU, every layer in one launch)
+// instead of transposing D and M for a grouped MFMA GEMM and refreshing the
+// operand copies layer by layer.
+constexpr int kHebbValuRows = 64;
 // K stagger of the settling phases and GEMMs with 16-bit operands: spreads
 // the tiles that share operand rows over 16 stage offsets (measured on 6 x 4096
 // and 12 x 8192 bf16 networks: 7-10% faster than no stagger, and better than 4
@@ -2142,9 +2147,51 @@ static int learn_step(pcd_model* m, const float* x0, const float* labels, const 
     }
 
     // Hebbian step of every layer (Layer.UpdateWeights, Layer.cs:320-333):
-    // W_l = (1 - eta_w lambda) (W_l + eta_w D_l^T M_l) as one grouped GEMM over
-    // the batch (K = rows; D_l and M_l transposed so K is contiguous), the
-    // bias sums, then the transposed copy W_l^T that the update phase reads.
+    // W_l = (1 - eta_w lambda) (W_l + eta_w D_l^T M_l), the bias sums, and the
+    // operand copies the settling reads (W_l^T; W_l for 16-bit models).
+    const float keep = 1.f - eta_w * weight_decay;
+    if (!st && batch <= kHebbValuRows) {
+        // A small batch: one launch of hebbian_small_kernel for all of it.
+        for (int l0 = 1; l0 < L && !st; l0 += kHebbLayers) {
+            HebbSet hs;
+            std::memset(&hs, 0, sizeof hs);
+            hs.batch = batch;
+            hs.alpha = eta_w * keep;
+            hs.beta = keep;
+            hs.eta_w = eta_w;
+            int blocks = 0;
+            for (int l = l0; l < L && hs.n < kHebbLayers; ++l) {
+                HebbLayer& h = hs.l[hs.n++];
+                h.d = w->D[l];
+                h.ldd = m->P[l - 1];
+                h.m = w->M[l];
+                h.ldm = m->P[l];
+                h.w = m->dtype == PCD_F32 ? (float*)m->W[l] : m->W32[l];
+                h.w16 = m->dtype == PCD_F32 ? nullptr : m->W[l];
+                h.ldw = m->P[l];
+                h.wt = m->WT[l];
+                h.ldwt = m->P[l - 1];
+                h.bias = m->bias[l];
+                h.lo = m->s[l - 1];
+                h.sz = m->s[l];
+                h.blocks = ((h.lo + 31) / 32) * ((h.sz + 31) / 32);
+                blocks += h.blocks;
+            }
+            switch (m->dtype) {
+            case PCD_F32: hipLaunchKernelGGL(hebbian_small_kernel<float>, dim3(blocks), dim3(256), 0, s, hs); break;
+            case PCD_BF16: hipLaunchKernelGGL(hebbian_small_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, hs); break;
+            default: hipLaunchKernelGGL(hebbian_small_kernel<f16_t>, dim3(blocks), dim3(256), 0, s, hs); break;
+            }
+            st = from_hip(hipGetLastError(), "hebbian_small_kernel launch");
+        }
+        if (energy_buf) {
+            int st2 = pool_free(energy_buf, s);
+            if (!st) st = st2;
+        }
+        return st;
+    }
+    // A larger batch: one grouped GEMM over the batch (K = rows; D_l and M_l
+    // transposed so K is contiguous), the bias sums, then the refreshed copies.
     const int kp = (int)round_up((size_t)batch, kFeatPad);
     std::vector<void*> tmp;
     std::vector<ProblemSet> sets;
@@ -2204,7 +2251,6 @@ static int learn_step(pcd_model* m, const float* x0, const float* labels, const 
         p.m = m->dtype == PCD_F32 ? (float*)m->W[l] : m->W32[l];   // fp32 weights or masters
     }
     if (!st) {
-        const float keep = 1.f - eta_w * weight_decay;
         PhaseArgs a;
         std::memset(&a, 0, sizeof a);
         a.alpha = eta_w * keep;

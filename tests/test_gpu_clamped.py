@@ -136,8 +136,10 @@ def test_classify_graph_and_eager_agree_bit_for_bit():
         assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("batch,wd", [(1, 0.0), (5, 0.0), (70, 0.01)])
+@pytest.mark.parametrize("batch,wd", [(1, 0.0), (5, 0.0), (64, 0.01), (70, 0.01)])
 def test_learn_step_fp32(oracle, batch, wd):
+    # up to 64 rows the weights are updated by the one-launch small-batch
+    # kernel, beyond by the grouped GEMM
     sizes = [37, 70, 19, 6]
     snap, W, b, P, x = build_case(sizes, "tanh", 0.1, batch=batch, bias_scale=0.1, seed=15)
     y = _one_hot(np.arange(batch) % 6, 6)
@@ -188,11 +190,14 @@ def test_train_two_patterns_then_predict(oracle):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
-def test_learn_step_16bit_masters(oracle, dtype):
-    # LearnMixed's scheme: 16-bit settling, fp32 master update, operands re-rounded
+@pytest.mark.parametrize("batch", [9, 100])
+def test_learn_step_16bit_masters(oracle, dtype, batch):
+    # LearnMixed's scheme: 16-bit settling, fp32 master update, operands
+    # re-rounded; a batch of 9 takes the one-launch small-batch update, 100 the
+    # grouped GEMM
     sizes = [37, 70, 19, 6]
-    snap, W, b, P, x = build_case(sizes, "gelu", 0.1, batch=9, bias_scale=0.1, seed=17)
-    y = _one_hot(np.arange(9) % 6, 6)
+    snap, W, b, P, x = build_case(sizes, "gelu", 0.1, batch=batch, bias_scale=0.1, seed=17)
+    y = _one_hot(np.arange(batch) % 6, 6)
     m = _model(snap, dtype)
     try:
         en = m.learn(x, y, 8, 0.05)
