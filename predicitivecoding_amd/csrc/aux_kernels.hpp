@@ -313,7 +313,8 @@ __global__ void bias_update_kernel(const void* __restrict__ d, int ld, int rows,
     }
 }
 
-// The learning step's weight and bias update for a small batch, every layer
+// The learning step's weight and bias update for a batch of at most a few
+// hundred rows, every layer
 // in one launch: W_l = beta W_l + alpha D_l^T M_l (K = the batch rows, summed
 // in row order on the VALU), b_l += eta_w * (column sums of D_l, rows in
 // order), and the refreshed operand copies W_l^T and, for 16-bit models,

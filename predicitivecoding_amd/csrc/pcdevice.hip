@@ -235,8 +235,9 @@ constexpr int kMinTileM = 32;   // rows of the shortest tile
 // Learning steps of at most this many rows update the weights with
 // hebbian_small_kernel (K = rows on the VALU, every layer in one launch)
 // instead of transposing D and M for a grouped MFMA GEMM and refreshing the
-// operand copies layer by layer.
-constexpr int kHebbValuRows = 64;
+// operand copies layer by layer (measured faster up to 512 rows on c1's and
+// c2's networks, slower at 1024 on c2's).
+constexpr int kHebbValuRows = 512;
 // K stagger of the settling phases and GEMMs with 16-bit operands: spreads
 // the tiles that share operand rows over 16 stage offsets (measured on 6 x 4096
 // and 12 x 8192 bf16 networks: 7-10% faster than no stagger, and better than 4
@@ -2151,7 +2152,7 @@ static int learn_step(pcd_model* m, const float* x0, const float* labels, const 
     // operand copies the settling reads (W_l^T; W_l for 16-bit models).
     const float keep = 1.f - eta_w * weight_decay;
     if (!st && batch <= kHebbValuRows) {
-        // A small batch: one launch of hebbian_small_kernel for all of it.
+        // At most kHebbValuRows rows: one launch of hebbian_small_kernel.
         for (int l0 = 1; l0 < L && !st; l0 += kHebbLayers) {
             HebbSet hs;
             std::memset(&hs, 0, sizeof hs);

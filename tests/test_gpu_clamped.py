@@ -136,10 +136,10 @@ def test_classify_graph_and_eager_agree_bit_for_bit():
         assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("batch,wd", [(1, 0.0), (5, 0.0), (64, 0.01), (70, 0.01)])
+@pytest.mark.parametrize("batch,wd", [(1, 0.0), (5, 0.0), (70, 0.01), (512, 0.0), (600, 0.01)])
 def test_learn_step_fp32(oracle, batch, wd):
-    # up to 64 rows the weights are updated by the one-launch small-batch
-    # kernel, beyond by the grouped GEMM
+    # up to 512 rows the weights are updated by the one-launch small-batch
+    # kernel (70 and 512 rows: several 64-row chunks), beyond by the grouped GEMM
     sizes = [37, 70, 19, 6]
     snap, W, b, P, x = build_case(sizes, "tanh", 0.1, batch=batch, bias_scale=0.1, seed=15)
     y = _one_hot(np.arange(batch) % 6, 6)
@@ -190,10 +190,10 @@ def test_train_two_patterns_then_predict(oracle):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("batch", [9, 100])
+@pytest.mark.parametrize("batch", [9, 600])
 def test_learn_step_16bit_masters(oracle, dtype, batch):
     # LearnMixed's scheme: 16-bit settling, fp32 master update, operands
-    # re-rounded; a batch of 9 takes the one-launch small-batch update, 100 the
+    # re-rounded; a batch of 9 takes the one-launch small-batch update, 600 the
     # grouped GEMM
     sizes = [37, 70, 19, 6]
     snap, W, b, P, x = build_case(sizes, "gelu", 0.1, batch=batch, bias_scale=0.1, seed=17)
