@@ -503,11 +503,15 @@ typedef const __attribute__((address_space(4))) Problem KProblem;
 // update epilogue per group, so each wave evaluates a quarter of the block's
 // activations and stores its four columns of each row directly (fp32 states,
 // operand-type deltas and state copies).  The error phase's row energies meet
-// across the groups through LDS, in group order.
+// across the groups through LDS, in group order.  `state` and `bias` are this
+// lane's four columns of the epilogue's state operand (M_{l-1} in the error
+// phase, X_l or the top layer's M_l in the update phase) and of the bias,
+// loaded by the caller before the K sweep.
 template <typename OP, int BM, int BN, int EPI>
-__device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArgs& args, const f32x16& acc, char* smem,
-                                                const int tile, const int split, const int ks, const int row0,
-                                                const int col0, const int tn) {
+__device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArgs& args, const f32x16& acc,
+                                                const f32x4 state, const f32x4 bias, char* smem, const int tile,
+                                                const int split, const int ks, const int row0, const int col0,
+                                                const int tn) {
     using C = TileCfg<BM, BN, OpTraits<OP>::bytes>;
     static_assert(C::KW == 4 && C::FM == 1 && C::FN == 1, "one block shared by four waves");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, half = lane >> 5;
@@ -602,8 +606,7 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
         }
     };
     if constexpr (EPI == EPI_ERROR) {
-        const f32x4 mv = gld4(P.mlow + idx);
-        const f32x4 bv = gld4(P.bias + col);
+        const f32x4 mv = state, bv = bias;   // M_{l-1} and b at (row, col .. col + 3)
         const float P_low = P.prec, inv2p = 0.5f / P.prec, eta = args.eta, lam = args.act_reg;
         f32x4 dv, xv;
         float es = 0.f;
@@ -649,7 +652,7 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
         // top layer reads M_l itself: M_l -= eta (lambda sign M_l - G).
         const float eta = args.eta, lam = args.act_reg;
         const bool folded = P.eself != nullptr;
-        const f32x4 xv = gld4((folded ? P.eself : P.m) + idx);
+        const f32x4 xv = state;   // X_l (or M_l at the top) at (row, col .. col + 3)
         f32x4 mn;
         static_for<0, 4>([&](auto K) PCD_INLINE {
             constexpr int k = decltype(K)::value;
@@ -785,6 +788,20 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         const bool any = *flag != 0;
         __syncthreads();
         if (!any) return;
+    }
+
+    // The K-shared tile's settling epilogue reads 16 bytes of one state row
+    // per lane (and, in the error phase, four biases): loaded here, their
+    // latency passes under the K sweep.
+    f32x4 epi_state{}, epi_bias{};
+    if constexpr (C::KW > 1 && (EPI == EPI_ERROR || EPI == EPI_UPDATE)) {
+        const size_t eidx = (size_t)(row0 + (lane & 31)) * P.ldo + col0 + 8 * wave + 4 * (lane >> 5);
+        if constexpr (EPI == EPI_ERROR) {
+            epi_state = gld4(P.mlow + eidx);
+            epi_bias = gld4(P.bias + col0 + 8 * wave + 4 * (lane >> 5));
+        } else {
+            epi_state = gld4((P.eself != nullptr ? P.eself : P.m) + eidx);
+        }
     }
 
     // ---- main loop
@@ -953,7 +970,8 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // this file with rows and columns exchanged).
     constexpr bool TR = EPI == EPI_ERROR || EPI == EPI_UPDATE;
     if constexpr (C::KW > 1 && TR) {
-        ksw_settle_tail<OP, BM, BN, EPI>(P, args, acc[0][0], smem, local, split, ks, row0, col0, tn);
+        ksw_settle_tail<OP, BM, BN, EPI>(P, args, acc[0][0], epi_state, epi_bias, smem, local, split, ks, row0, col0,
+                                         tn);
         return;
     }
     if constexpr (C::KW > 1) {
