@@ -573,7 +573,11 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
     const int L = m->L;
     const int tm = (batch + tile.m - 1) / tile.m;
     int slot = 0;
-    for (int l = L - 1; l >= 1; --l) {   // error phase: widest K first is irrelevant; keep layer order
+    // Error phase, layers in ascending order: the energy slots then follow
+    // e_0, e_1, ... in the order the reference forms the layer errors
+    // (BatchedPcForward.cs:100-107), and the order measured 1% faster than
+    // descending on c5s (0.5% on c1).
+    for (int l = 1; l < L; ++l) {
         if (err.empty() || err.back().n == kMaxProblems) { err.emplace_back(); err.back().n = 0; }
         ProblemSet& ps = err.back();
         Problem& p = ps.p[ps.n++];
