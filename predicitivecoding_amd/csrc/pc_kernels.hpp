@@ -574,9 +574,9 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
         g = sum;
     }
 
-    // Row lr of the block, columns col .. col + 3.  The operands are read
-    // whatever the row's state (rows and columns are padded in memory, the
-    // padding is zero); only valid rows and columns below N are written.
+    // Row lr of the block, columns col .. col + 3.  The caller read `state` and
+    // `bias` whatever the row's state (rows and columns are padded in memory,
+    // the padding is zero); only valid rows and columns below N are written.
     const int row = row0 + lr, col = col0 + 8 * wave + 4 * half;
     const bool rok = row < P.M && row_active(args, row);
     const bool cfull = col + 3 < P.N;
