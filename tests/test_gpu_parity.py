@@ -48,6 +48,20 @@ def test_activations_and_options_fp32(oracle, act, variant):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("tile", [32, 64])
+def test_16bit_ffg_warm_start(oracle, dtype, tile):
+    # the feed-forward warm start on 16-bit operands, on the K-shared tile (its
+    # all-reduce epilogue) and on 64 x 64, against the same-rounding oracle
+    snap, W, b, P, x = build_case([37, 70, 19, 5], "tanh", 0.1, batch=13, bias_scale=0.2, seed=31, ffg=True)
+    top, st, en = run_gpu(snap, x, 10, dtype=dtype, states=True, energy=True, options={"tile": tile})
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 10, dtype=dtype, states=True, energy=True)
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren),
+                states=max(max_rel(a, r) for a, r in zip(st, rst)))
+    _report(f"ffg/{dtype}/tile{tile}", **errs)
+    assert all(v < 2e-3 for v in errs.values()), errs
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("act", ["tanh", "gelu"])
 def test_16bit_operands(oracle, dtype, act):
     snap, W, b, P, x = build_case([96, 130, 64, 16], act, 0.05, batch=40, init="fanin", seed=5)
