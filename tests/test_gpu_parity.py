@@ -530,14 +530,16 @@ def test_c4_ragged_full_network(oracle, rule, thr):
         assert all(v < 1e-4 for v in errs.values()), errs
 
 
-def test_c4_exit_fires_at_full_scale(oracle):
+@pytest.mark.parametrize("rule,thr", [("absolute", 560.0), ("relative", 1e-2)])
+def test_c4_exit_fires_at_full_scale(oracle, rule, thr):
     # BASELINE configs[3] exactly (64 requests, 4 x 2048 tanh fp32, its rows
-    # and budgets), with an absolute threshold the energies do cross: C4's own
-    # 1e-3 per sample is never reached (energy per sample is still ~517 after
-    # 64 steps, inputs N(0,1) over 2048 units), so 560 per sample, which
-    # requests reach after about 25 steps.  Some requests must leave before
-    # their budget; each checked request's exit step, energy and top states
-    # equal the oracle settling that request alone.
+    # and budgets), with thresholds the energies do cross: C4's own 1e-3 per
+    # sample is never reached (energy per sample is still ~517 after 64 steps,
+    # inputs N(0,1) over 2048 units), so 560 per sample, which requests reach
+    # after about 25 steps; and the relative rule at 1e-2 (the bench's c4x).
+    # Some requests must leave before their budget; each checked request's
+    # exit step, energy and top states equal the oracle settling that request
+    # alone.
     import bench
     from predicitivecoding_amd import PcDeviceModel
     cfg = bench.CONFIGS["c4"]
@@ -547,11 +549,11 @@ def test_c4_exit_fires_at_full_scale(oracle):
     x = np.random.default_rng(22).standard_normal((int(offsets[-1]), sizes[0])).astype(np.float32)
     m = PcDeviceModel(snap, "f32")
     try:
-        used, fe, top = m.relax_ragged(x, offsets, steps, "absolute", 560.0)
+        used, fe, top = m.relax_ragged(x, offsets, steps, rule, thr)
     finally:
         m.close()
     early = np.flatnonzero(used < steps)
-    _report(f"c4/absolute 560: {len(early)} of {len(steps)} requests exited early",
+    _report(f"c4/{rule} {thr}: {len(early)} of {len(steps)} requests exited early",
             mean_used=float(used.mean()), mean_budget=float(steps.mean()))
     assert len(early) >= 8, (used, steps)
     assert np.all(used >= 1) and np.all(used <= steps)
@@ -563,9 +565,9 @@ def test_c4_exit_fires_at_full_scale(oracle):
     for r in check:
         lo, hi = int(offsets[r]), int(offsets[r + 1])
         rused, rfe, rtop = oracle.ragged_relax(sizes, "tanh", cfg["eta"], W, b, P, x[lo:hi], [0, hi - lo],
-                                               [int(steps[r])], "absolute", 560.0)
+                                               [int(steps[r])], rule, thr)
         errs = dict(top=max_rel(top[lo:hi], rtop), energy=max_rel(fe[r:r + 1], rfe))
-        _report(f"c4/absolute 560/request{r} rows={hi - lo} steps={steps[r]} used={used[r]}", **errs)
+        _report(f"c4/{rule} {thr}/request{r} rows={hi - lo} steps={steps[r]} used={used[r]}", **errs)
         assert used[r] == rused[0], (r, used[r], rused[0])
         assert all(v < 1e-4 for v in errs.values()), errs
 
