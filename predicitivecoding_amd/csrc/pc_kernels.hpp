@@ -703,9 +703,12 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     const bool writer = C::KW == 1 || wave == 0;
 
     // Energy of the previous error phase, reduced per row in a fixed order
-    // before any tile work (deterministic, no atomics).
+    // before any tile work (deterministic, no atomics).  The rows go to the
+    // last virtual blocks, which run the last problems' tiles (or none): the
+    // first problem, the one with the longest K sweep in the small networks
+    // whose phases are latency-bound, then starts without this delay.
     if (EPI == EPI_UPDATE && args.energy_out != nullptr) {
-        for (int row = vblock * C::NT + tid; row < args.batch; row += vgrid * C::NT) {
+        for (int row = (vgrid - 1 - vblock) * C::NT + tid; row < args.batch; row += vgrid * C::NT) {
             gst(args.energy_out + (size_t)args.t * args.batch + row,
                 sum_slots(args.energy_part, args.ldp, args.nslots, row));
         }
