@@ -15,6 +15,23 @@ __global__ void zero_kernel(u32x4* __restrict__ p, size_t n) {
     for (; i < n; i += stride) p[i] = u32x4{0u, 0u, 0u, 0u};
 }
 
+// Zero-fill of up to kZeroSegs buffers (n[k] 16-byte units at p[k]) in one
+// launch: the free states a settling starts from, every layer in one node.
+constexpr int kZeroSegs = 32;
+struct ZeroSegs {
+    u32x4* p[kZeroSegs];
+    size_t n[kZeroSegs];
+    int count;
+};
+__global__ void zero_segs_kernel(const ZeroSegs z) {
+    const size_t i0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (int k = 0; k < z.count; ++k) {
+        u32x4* p = z.p[k];
+        for (size_t i = i0; i < z.n[k]; i += stride) p[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
 // Pack a row-major [rows x cols] fp32 matrix (optionally read transposed) into
 // a zero-padded [prow x pcol] buffer of the operand type whose rows are `ldd`
 // elements apart (ldd >= pcol; the columns past pcol are left alone).

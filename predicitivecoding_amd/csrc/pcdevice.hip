@@ -225,6 +225,31 @@ int launch_zero(void* p, size_t bytes, hipStream_t s) {
     return from_hip(hipGetLastError(), "zero_kernel launch");
 }
 
+// Buffers to zero, gathered and cleared by one zero_segs_kernel launch per
+// kZeroSegs of them.
+struct ZeroBatch {
+    ZeroSegs z{};
+    size_t most = 0;   // units of the largest buffer gathered
+    int add(void* p, size_t bytes, hipStream_t s) {
+        const size_t units = bytes / 16;
+        if (units == 0) return PCD_SUCCESS;
+        if (z.count == kZeroSegs)
+            if (int st = flush(s)) return st;
+        z.p[z.count] = (u32x4*)p;
+        z.n[z.count++] = units;
+        most = std::max(most, units);
+        return PCD_SUCCESS;
+    }
+    int flush(hipStream_t s) {
+        if (z.count == 0) return PCD_SUCCESS;
+        const int grid = (int)std::min<size_t>((most + 255) / 256, 4096);
+        hipLaunchKernelGGL(zero_segs_kernel, dim3(grid), dim3(256), 0, s, z);
+        z.count = 0;
+        most = 0;
+        return from_hip(hipGetLastError(), "zero_segs_kernel launch");
+    }
+};
+
 inline int op_bytes(int dtype) { return dtype == PCD_F32 ? 4 : 2; }
 
 // --------------------------------------------------------------- PC model
@@ -723,12 +748,14 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
     const int batch = r.batch;
     const Tile tile = r.tile;
     int st;
+    ZeroBatch zb;
     for (int l = 1; l < L; ++l) {
         if (l == L - 1 && r.clamp_top) break;
         if (l <= L - 2 && r.keep_hidden) continue;
-        if ((st = launch_zero(w->M[l], (size_t)w->cap * m->P[l] * 4, s))) return st;
-        if (w->S[l] && (st = launch_zero(w->S[l], (size_t)w->cap * m->P[l] * op_bytes(m->dtype), s))) return st;
+        if ((st = zb.add(w->M[l], (size_t)w->cap * m->P[l] * 4, s))) return st;
+        if (w->S[l] && (st = zb.add(w->S[l], (size_t)w->cap * m->P[l] * op_bytes(m->dtype), s))) return st;
     }
+    if ((st = zb.flush(s))) return st;
     std::vector<ProblemSet> err, upd;
     int nslots = 0;
     build_phase_sets(m, w, batch, tile, r.clamp_top, err, upd, &nslots);
