@@ -167,19 +167,26 @@ enum TileOrder { TILE_INTERLEAVED = 0, TILE_CONTIGUOUS = 1 };
 // only where |tanh| is below ~1e-3, where the absolute error is what the
 // relaxation sees); saturates to +-1 for large |x|.
 __device__ __forceinline__ float fast_tanh(float x) {
+#pragma clang fp contract(off)
     const float e = __builtin_amdgcn_exp2f(fabsf(x) * 2.8853900817779268f);  // exp(2|x|)
-    const float t = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
+    const float t = __builtin_fmaf(-2.f, __builtin_amdgcn_rcpf(e + 1.f), 1.f);
     return copysignf(t, x);
 }
 
 // f(pre) and f'(pre) together (Activation.cs:34-132; GELU-tanh and its
 // derivative from pre, Layers.cs:42-50 and Autograd.cs:313-318), sharing the
-// one transcendental evaluation both need.
+// one transcendental evaluation both need.  Multiply-adds are written out
+// (fmaf) and nothing else is contracted, here or in fast_tanh, so f(pre) has
+// the same bits in every epilogue whether or not f'(pre) is used beside it:
+// the FFG warm start's M_{l-1} = f(W_l M_l + b) and the first error phase's f
+// of the same pre-activation must agree exactly (their difference is the
+// error, exactly zero in the reference).
 __device__ __forceinline__ void act_eval(int act, float x, float& y, float& dy) {
+#pragma clang fp contract(off)
     switch (act) {
     case ACT_TANH: {
         y = fast_tanh(x);
-        dy = 1.f - y * y;
+        dy = __builtin_fmaf(-y, y, 1.f);
         break;
     }
     case ACT_RELU:
@@ -188,15 +195,17 @@ __device__ __forceinline__ void act_eval(int act, float x, float& y, float& dy) 
         break;
     case ACT_SIGMOID: {
         y = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
-        dy = y * (1.f - y);
+        dy = __builtin_fmaf(-y, y, y);
         break;
     }
     case ACT_GELU: {
         const float c = 0.7978845608f, a = 0.044715f;
         const float x2 = x * x;
-        const float t = fast_tanh(c * (x + a * x2 * x));
-        y = 0.5f * x * (1.f + t);
-        dy = 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * (c * (1.f + 3.f * a * x2));
+        const float t = fast_tanh(c * __builtin_fmaf(a * x2, x, x));   // tanh(c (x + a x^3))
+        const float h = 0.5f * x;
+        y = __builtin_fmaf(h, t, h);                                     // x (1 + t) / 2
+        const float slope = c * __builtin_fmaf(3.f * a, x2, 1.f);        // d/dx of c (x + a x^3)
+        dy = __builtin_fmaf(h * __builtin_fmaf(-t, t, 1.f), slope, __builtin_fmaf(0.5f, t, 0.5f));
         break;
     }
     default:

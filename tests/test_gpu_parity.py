@@ -61,6 +61,33 @@ def test_16bit_ffg_warm_start(oracle, dtype, tile):
     assert all(v < 2e-3 for v in errs.values()), errs
 
 
+@pytest.mark.parametrize("tile", [32, 64])
+@pytest.mark.parametrize("act", ["tanh", "sigmoid", "gelu", "relu"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_ffg_start_leaves_the_free_top_exactly_zero(oracle, dtype, act, tile):
+    # The FFG warm start sets each hidden layer to f(W M + b) of the layer
+    # above, the free top at zero, so the first error phase's errors above
+    # layer 0 are exactly zero and the top stays exactly zero through step 1;
+    # step 2's lambda sign(M_top) term then sees sign(0) = 0, as in the oracle.
+    # The warm start and the error phase must give f the same bits: a one-ulp
+    # difference leaves the top at ~1e-12 and moves it by lambda eta at step 2.
+    sizes = [127, 257, 129, 1, 257]
+    snap, W, b, P, x = build_case(sizes, act, 0.08, act_reg=0.01, ffg=True, batch=64, seed=9097, bias_scale=0.5)
+    opts = {"tile": tile}
+    _, st1, _ = run_gpu(snap, x, 1, dtype=dtype, states=True, energy=True, options=opts)
+    _, rst1, _ = run_oracle(oracle, snap, W, b, P, x, 1, dtype=dtype, states=True, energy=True)
+    assert np.all(rst1[-1] == 0)
+    nz = int(np.count_nonzero(st1[-1]))
+    print(f"ffg top {dtype}/{act}/tile{tile}: {nz} nonzero top elements after step 1", flush=True)
+    assert nz == 0
+    top, st, en = run_gpu(snap, x, 6, dtype=dtype, states=True, energy=True, options=opts)
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 6, dtype=dtype, states=True, energy=True)
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren),
+                states=max(max_rel(a, r) for a, r in zip(st, rst)))
+    _report(f"ffg-top/{dtype}/{act}/tile{tile}", **errs)
+    assert all(v < (1e-4 if dtype == "f32" else 2e-3) for v in errs.values()), errs
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("act", ["tanh", "gelu"])
 def test_16bit_operands(oracle, dtype, act):

@@ -246,6 +246,24 @@ def test_oracle_matches_autograd(oracle, act, ffg, act_reg):
     assert close(en32, en_ref, 1e-5)
 
 
+@pytest.mark.parametrize("act", ACTS)
+def test_ffg_start_keeps_the_free_top_exactly_zero(oracle, act):
+    # With the FFG warm start every hidden layer starts at f of its prediction
+    # from the (zero) layer above, so step 1's errors above layer 0 vanish and
+    # the free top's update is exactly zero: the top is 0 after step 1 in both
+    # restatements.  On this network it leaves zero at step 2, once lambda
+    # sign(M) has moved the layer below off its warm start.
+    sizes = [9, 13, 7, 1, 6]
+    W, b, P = make_net(sizes, seed=23, bias_scale=0.5)
+    x = make_inputs(4, 9, seed=24)
+    for T, zero in ((1, True), (2, False)):
+        _, st, _ = oracle.persample_relax_f64(sizes, act, 0.08, W, b, P, x, T, act_reg=0.01, ffg=True,
+                                              want_states=True)
+        _, st32, _ = oracle.batched_relax(sizes, act, 0.08, W, b, P, x, T, act_reg=0.01, ffg=True,
+                                          want_states=True)
+        assert np.all(st[-1] == 0) == zero and np.all(st32[-1] == 0) == zero
+
+
 def test_batched_matches_per_sample_reference_tolerance(oracle):
     # BatchedPcForwardTests.cs:44-72 shape: [6,10,4] tanh, eta 0.1, inputs U(-1,1), T=15
     sizes = [6, 10, 4]
