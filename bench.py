@@ -24,6 +24,14 @@ Workloads:
   c1learn  c1's network taking a learning step (Network.Learn) on a batch of
            64 labelled samples; value counts 64 rows x T.
   gemm     the GEMM provider (pcd_gemm_bf16) on 8192^3, in TFLOP/s.
+  pub      the reference's own published workload (MixedPrecisionBench):
+           [3072,512,128,10] tanh, eta 0.05, 64 inputs, T=20, host arrays in
+           and out through the drop-in, median of repeated calls, beside the
+           published RTX 4070 SUPER / Ryzen figures.
+
+The default line (c5) also carries, under "extra", the c3 record (the
+configuration the bf16 target is stated on) and the pub record, and under
+"pcie_inclusive" the c5 pass with its input and output on the host.
 
 The JSON line carries the roofline of the dominant kernel (average duration
 of its launches from HIP events on the library's stream) and a CPU baseline:
@@ -75,6 +83,13 @@ CONFIGS = {
     "c5s": dict(sizes=[8192] * 12, act=4, dtype="bf16", batch=64, T=16, eta=0.02, x="normal", init="fanin"),
     # the GEMM provider slot (IGemmProvider / CudaGemmProvider.MatMulDeviceExBf16) on c5's layer shape
     "gemm": dict(dtype="bf16", m=8192, k=8192, n=8192),
+    # the reference's own published batched-forward workload (tools/MixedPrecisionBench/Program.cs:75-127):
+    # [3072,512,128,10] tanh, StateLearningRate 0.05, 64 inputs ~N(0,1), 20 steps, host arrays in and out;
+    # published (ROADMAP-MixedPrecision.md:99, Ryzen-class CPU + RTX 4070 SUPER): per-sample loop 574 ms,
+    # batched CPU 158 ms, batched CUDA float 75 ms, CUDA mixed (fp16) 94 ms per call
+    "pub": dict(sizes=[3072, 512, 128, 10], act=1, dtype="f32", batch=64, T=20, eta=0.05, x="normal",
+                init="xavier", published_ms={"per_sample_loop": 574.0, "cpu_batched": 158.0, "cuda_float": 75.0,
+                                             "cuda_mixed": 94.0}),
 }
 ACT_NAME = {1: "tanh", 4: "gelu"}
 
@@ -650,6 +665,241 @@ def cpu_baseline_ragged(cfg, W, b, x_host, offsets, steps, budget_s=10.0):
 
 
 
+def median_ms_of(run, reps, warmup=1):
+    """Median wall time of `run` in ms over `reps` calls after `warmup` untimed
+    ones (the reference harness's MedianMs, Program.cs:96-101)."""
+    for _ in range(warmup):
+        run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)) * 1e3
+
+
+def bench_published(args, standalone=False):
+    """pub: the reference's published batched-forward workload, timed as its
+    harness times it: one call of the drop-in (host arrays in and out,
+    BatchedPcForward.infer_get_top_batch, float and mixed) per repetition, the
+    median after a warm-up, beside the oracle's batched fp32 path (the
+    reference's CpuGemmProvider route) and its per-sample loop on the host
+    cores.  The reference's .NET Random streams cannot be reproduced: weights
+    are seeded Xavier-normal as Network's tanh initialiser draws them, inputs
+    seeded N(0, 1)."""
+    import torch
+    from predicitivecoding_amd import BatchedPcForward, GenerativeSnapshot, PcDeviceModel
+    cfg = CONFIGS["pub"]
+    sizes, B, T, eta = cfg["sizes"], cfg["batch"], cfg["T"], cfg["eta"]
+    print(f"# bench pub: sizes={sizes} B={B} T={T} tanh f32, host arrays (the reference's published workload)",
+          file=sys.stderr, flush=True)
+    W, b = make_weights(cfg)
+    rng = np.random.default_rng(4)
+    inputs = [rng.standard_normal(sizes[0]).astype(np.float32) for _ in range(B)]
+    snap = GenerativeSnapshot(sizes, cfg["act"], eta, 0.0, False, W, b, [1.0] * len(sizes))
+    reps = max(3, args.steps)
+    ms_float = median_ms_of(lambda: BatchedPcForward.infer_get_top_batch(snap, inputs, T), reps)
+    ms_mixed = median_ms_of(lambda: BatchedPcForward.infer_get_top_batch(snap, inputs, T, mixed=True), reps)
+    # the same settling on inputs already in HBM (the kernels alone, one pass)
+    model = PcDeviceModel(snap, "f32")
+    x = torch.from_numpy(np.stack(inputs)).cuda()
+    top = torch.empty((B, sizes[-1]), device="cuda", dtype=torch.float32)
+
+    def resident():
+        model.relax_device(x.data_ptr(), B, T, top.data_ptr())
+        torch.cuda.synchronize()
+
+    ms_resident = median_ms_of(resident, reps)
+    model.close()
+    pub = cfg["published_ms"]
+    print(f"# pub: drop-in float {ms_float:.3f} ms, mixed {ms_mixed:.3f} ms, resident {ms_resident:.3f} ms per call "
+          f"(published CUDA float {pub['cuda_float']} ms, mixed {pub['cuda_mixed']} ms)", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import pc_oracle
+        threads = cpu_threads()
+        pc_oracle.set_threads(threads)
+        P = [1.0] * len(sizes)
+        xs = np.stack(inputs)
+        ms_batched = median_ms_of(lambda: pc_oracle.batched_relax(sizes, "tanh", eta, W, b, P, xs, T), CPU_REPS)
+        pc_oracle.set_threads(1)
+        ms_loop = median_ms_of(lambda: [pc_oracle.batched_relax(sizes, "tanh", eta, W, b, P, xs[i:i + 1], T)
+                                        for i in range(B)], CPU_REPS)
+        cpu = {"value": B * T / (ms_batched * 1e-3), "unit": "sample-steps/s", "cores": threads,
+               **host_fields(threads), "kind": "port",
+               "batched_ms": ms_batched, "per_sample_loop_ms": ms_loop, "per_sample_loop_threads": 1,
+               "sample": f"the whole workload: oracle batched fp32 relaxation of the {B} inputs x {T} steps on "
+                         f"{threads} threads (median of {CPU_REPS} after 1 warm-up), and the per-sample loop "
+                         f"({B} batch-1 settlings, 1 thread)"}
+        print(f"# pub cpu: batched {ms_batched:.1f} ms on {threads} threads, per-sample loop {ms_loop:.1f} ms",
+              file=sys.stderr, flush=True)
+    rec = {
+        "metric": "relaxed samples*steps/sec at 1 GPU and % of MFMA/HBM roofline",
+        "value": B * T / (ms_float * 1e-3), "unit": "sample-steps/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "ms_per_step": ms_float, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded Xavier-normal weights, N(0,1) inputs)",
+        "config": {"workload": f"pub: {topology(sizes)} tanh f32, B={B}, T={T}, eta={eta}, host arrays through "
+                               "BatchedPcForward.infer_get_top_batch (tools/MixedPrecisionBench/Program.cs:75-127)",
+                   "batch": B, "relax_steps": T, "layer_sizes": sizes, "parallelism": "single GPU"},
+        "ms_per_call": {"dropin_float": ms_float, "dropin_mixed_f16": ms_mixed, "device_resident_float": ms_resident},
+        "published_ms": {**pub, "hardware": "Ryzen-class CPU + RTX 4070 SUPER",
+                         "source": "PredicitiveCoding/ROADMAP-MixedPrecision.md:99"},
+        "speedup_vs_published": {"cuda_float": pub["cuda_float"] / ms_float,
+                                 "cuda_mixed": pub["cuda_mixed"] / ms_mixed,
+                                 "cpu_batched": pub["cpu_batched"] / ms_float},
+        "cpu_baseline": cpu,
+    }
+    if not standalone:
+        for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline"):
+            rec.pop(k)
+    return rec
+
+
+def bench_settle(args, name, cfg, steps, warmup, cpu_budget, pcie=False):
+    """One fixed-batch settling workload (c1, c2, c3, c5, c5s): `steps` timed
+    passes of pcd_pc_relax on inputs resident in HBM after `warmup` untimed
+    ones, the per-phase roofline from HIP events, optionally the same pass
+    with host input and output (pcie), and the CPU baseline.  Returns the
+    record."""
+    import torch
+    from predicitivecoding_amd import GenerativeSnapshot, PcDeviceModel
+    sizes, B, T = cfg["sizes"], cfg["batch"], cfg["T"]
+    print(f"# bench {name}: sizes={sizes} B={B} T={T} dtype={cfg['dtype']}", file=sys.stderr, flush=True)
+    W, b = make_weights(cfg)
+    snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
+    model = PcDeviceModel(snap, cfg["dtype"])
+    apply_options(model, args)
+    if args.tile_order >= 0:
+        model.set_option("tile_order", args.tile_order)
+    if args.tile:
+        model.set_option("tile", args.tile)
+        if args.tile_n:
+            model.set_option("tile_n", args.tile_n)
+    x = make_inputs(cfg)
+    top = torch.empty((B, sizes[-1]), device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+
+    def one_pass():
+        model.relax_device(x.data_ptr(), B, T, top.data_ptr())
+
+    for _ in range(warmup):
+        one_pass()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one_pass()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / steps
+    value = B * T * steps / elapsed
+    print(f"# timed {steps} passes: {ms_per_step:.3f} ms/pass, {value:.4g} sample-steps/s",
+          file=sys.stderr, flush=True)
+
+    # Roofline: the same passes again with HIP events around every phase launch
+    # (eager launches on the library's stream), averaged per phase.
+    model.set_option("profile", 1)
+    err_ms = upd_ms = 0.0
+    launches = 0
+    for _ in range(max(1, min(steps, 5))):
+        one_pass()
+        e, u, n = model.profile_result()
+        err_ms += e * n
+        upd_ms += u * n
+        launches += n
+    torch.cuda.synchronize()
+    model.set_option("profile", 0)
+    err_ms /= launches
+    upd_ms /= launches
+    dom_name, dom_ms = ("update_phase", upd_ms) if upd_ms >= err_ms else ("error_phase", err_ms)
+    flop_launch = 2.0 * B * sum(sizes[l] * sizes[l - 1] for l in range(1, len(sizes)))
+    bytes_err, bytes_upd = phase_bytes(sizes, B, cfg["dtype"])
+    bytes_launch = bytes_upd if dom_name == "update_phase" else bytes_err
+    peak = PEAK[cfg["dtype"]]
+    # The roofline the arithmetic names: HBM when the launch's FLOP per
+    # algorithmic byte is below the ridge (peak FLOP/s / peak HBM bytes/s).
+    if flop_launch / bytes_launch < peak / HBM_PEAK:
+        achieved = bytes_launch / (dom_ms * 1e-3)
+        roofline = {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                    "frac": achieved / HBM_PEAK, "traffic": traffic_from_profiles(name, dom_name),
+                    "kernel": dom_name, "kernel_ms": dom_ms, "error_phase_ms": err_ms, "update_phase_ms": upd_ms,
+                    "bytes_per_launch": bytes_launch, "flop_per_launch": flop_launch,
+                    "mfma_frac": flop_launch / (dom_ms * 1e-3) / peak, "launches_timed": launches}
+        print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch; {dom_name} at "
+              f"{achieved / 1e9:.0f} GB/s = {100 * achieved / HBM_PEAK:.1f}% of HBM peak", file=sys.stderr,
+              flush=True)
+    else:
+        achieved = flop_launch / (dom_ms * 1e-3)
+        roofline = {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                    "frac": achieved / peak, "traffic": traffic_from_profiles(name, dom_name),
+                    "kernel": dom_name, "kernel_ms": dom_ms, "error_phase_ms": err_ms, "update_phase_ms": upd_ms,
+                    "flop_per_launch": flop_launch, "bytes_per_launch": bytes_launch, "launches_timed": launches,
+                    "path_frac": (flops_per_sample_step(sizes) * value) / peak,
+                    # the same launch against the HBM roofline: algorithmic bytes / duration
+                    "hbm_achieved_GBps": bytes_launch / (dom_ms * 1e-3) / 1e9,
+                    "hbm_frac": bytes_launch / (dom_ms * 1e-3) / HBM_PEAK}
+        print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch; {dom_name} at "
+              f"{achieved / 1e12:.1f} TFLOP/s = {100 * achieved / peak:.1f}% of peak, "
+              f"{bytes_launch / (dom_ms * 1e-3) / 1e9:.0f} GB/s algorithmic", file=sys.stderr, flush=True)
+    roofline.update(traffic_fields(sizes, B, cfg["dtype"]))
+
+    pcie_rec = None
+    if pcie:
+        # The same passes with the input on the host and the top states back
+        # on the host (pinned buffers): one H2D of x0 and one D2H of the top
+        # per pass, as a caller handing over host arrays pays.  Reported beside
+        # `value`, which keeps the inputs resident in HBM.
+        x_pin = torch.empty((B, sizes[0]), dtype=torch.float32, pin_memory=True)
+        x_pin.copy_(x)
+        top_pin = torch.empty((B, sizes[-1]), dtype=torch.float32, pin_memory=True)
+        torch.cuda.synchronize()
+        n_pcie = max(1, min(steps, 5))
+        t0 = time.perf_counter()
+        for _ in range(n_pcie):
+            x.copy_(x_pin, non_blocking=True)
+            one_pass()
+            top_pin.copy_(top, non_blocking=True)
+            torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / n_pcie
+        pcie_rec = {"value": B * T / dt, "unit": "sample-steps/s", "ms_per_step": dt * 1e3, "passes": n_pcie,
+                    "h2d_bytes": B * sizes[0] * 4, "d2h_bytes": B * sizes[-1] * 4,
+                    "what": "host x0 (pinned) -> H2D -> settle -> D2H top (pinned) -> synchronize, per pass"}
+        print(f"# pcie-inclusive: {dt * 1e3:.3f} ms/pass, {B * T / dt:.4g} sample-steps/s", file=sys.stderr,
+              flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        x_host = x.cpu().numpy()
+        cpu = cpu_baseline(cfg, W, b, x_host, cpu_budget)
+        print(f"# cpu baseline: {cpu['value']:.4g} sample-steps/s on {cpu['cores']} threads", file=sys.stderr,
+              flush=True)
+
+    rec = {
+        "metric": "relaxed samples*steps/sec at 1 GPU and % of MFMA/HBM roofline",
+        "value": value,
+        "unit": "sample-steps/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic (seeded random weights and inputs)",
+        "config": {"workload": f"{name}: {topology(sizes)} {ACT_NAME[cfg['act']]} "
+                               f"{cfg['dtype']}, B={B}, T={T}, eta={cfg['eta']}",
+                   "batch": B, "relax_steps": T, "layer_sizes": sizes, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    if pcie_rec is not None:
+        rec["pcie_inclusive"] = pcie_rec
+    model.close()
+    return rec
+
+
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -657,6 +907,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="default (c5) line only: leave out the c3 and published-workload records")
     ap.add_argument("--cpu-budget", type=float, default=20.0,
                     help="seconds the CPU baseline sample is sized for (its calibration overestimates ~2x)")
     ap.add_argument("--tile", type=int, default=0, help="force the GEMM tile rows (and columns unless --tile-n)")
@@ -683,10 +935,10 @@ def main():
         calibrate_copy()
         return
 
-    import torch
-    from predicitivecoding_amd import GenerativeSnapshot, PcDeviceModel
-
     cfg = CONFIGS[args.config]
+    if args.config == "pub":
+        print(json.dumps(bench_published(args, standalone=True)))
+        return
     if "requests" in cfg:
         bench_ragged(args, cfg)
         return
@@ -696,113 +948,15 @@ def main():
     if args.config == "gemm":
         bench_gemm(args, cfg)
         return
-    sizes, B, T = cfg["sizes"], cfg["batch"], cfg["T"]
-    print(f"# bench {args.config}: sizes={sizes} B={B} T={T} dtype={cfg['dtype']}", file=sys.stderr, flush=True)
-    W, b = make_weights(cfg)
-    snap = GenerativeSnapshot(sizes, cfg["act"], cfg["eta"], 0.0, False, W, b, [1.0] * len(sizes))
-    model = PcDeviceModel(snap, cfg["dtype"])
-    apply_options(model, args)
-    if args.tile_order >= 0:
-        model.set_option("tile_order", args.tile_order)
-    if args.tile:
-        model.set_option("tile", args.tile)
-        if args.tile_n:
-            model.set_option("tile_n", args.tile_n)
-    x = make_inputs(cfg)
-    top = torch.empty((B, sizes[-1]), device="cuda", dtype=torch.float32)
-    torch.cuda.synchronize()
-
-    def one_pass():
-        model.relax_device(x.data_ptr(), B, T, top.data_ptr())
-
-    for _ in range(args.warmup):
-        one_pass()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        one_pass()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
-    value = B * T * args.steps / elapsed
-    print(f"# timed {args.steps} passes: {ms_per_step:.3f} ms/pass, {value:.4g} sample-steps/s",
-          file=sys.stderr, flush=True)
-
-    # Roofline: the same passes again with HIP events around every phase launch
-    # (eager launches on the library's stream), averaged per phase.
-    model.set_option("profile", 1)
-    err_ms = upd_ms = 0.0
-    launches = 0
-    for _ in range(max(1, min(args.steps, 5))):
-        one_pass()
-        e, u, n = model.profile_result()
-        err_ms += e * n
-        upd_ms += u * n
-        launches += n
-    torch.cuda.synchronize()
-    model.set_option("profile", 0)
-    err_ms /= launches
-    upd_ms /= launches
-    dom_name, dom_ms = ("update_phase", upd_ms) if upd_ms >= err_ms else ("error_phase", err_ms)
-    flop_launch = 2.0 * B * sum(sizes[l] * sizes[l - 1] for l in range(1, len(sizes)))
-    bytes_err, bytes_upd = phase_bytes(sizes, B, cfg["dtype"])
-    bytes_launch = bytes_upd if dom_name == "update_phase" else bytes_err
-    peak = PEAK[cfg["dtype"]]
-    # The roofline the arithmetic names: HBM when the launch's FLOP per
-    # algorithmic byte is below the ridge (peak FLOP/s / peak HBM bytes/s).
-    if flop_launch / bytes_launch < peak / HBM_PEAK:
-        achieved = bytes_launch / (dom_ms * 1e-3)
-        roofline = {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                    "frac": achieved / HBM_PEAK, "traffic": traffic_from_profiles(args.config, dom_name),
-                    "kernel": dom_name, "kernel_ms": dom_ms, "error_phase_ms": err_ms, "update_phase_ms": upd_ms,
-                    "bytes_per_launch": bytes_launch, "flop_per_launch": flop_launch,
-                    "mfma_frac": flop_launch / (dom_ms * 1e-3) / peak, "launches_timed": launches}
-        print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch; {dom_name} at "
-              f"{achieved / 1e9:.0f} GB/s = {100 * achieved / HBM_PEAK:.1f}% of HBM peak", file=sys.stderr,
-              flush=True)
-    else:
-        achieved = flop_launch / (dom_ms * 1e-3)
-        roofline = {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
-                    "frac": achieved / peak, "traffic": traffic_from_profiles(args.config, dom_name),
-                    "kernel": dom_name, "kernel_ms": dom_ms, "error_phase_ms": err_ms, "update_phase_ms": upd_ms,
-                    "flop_per_launch": flop_launch, "bytes_per_launch": bytes_launch, "launches_timed": launches,
-                    "path_frac": (flops_per_sample_step(sizes) * value) / peak,
-                    # the same launch against the HBM roofline: algorithmic bytes / duration
-                    "hbm_achieved_GBps": bytes_launch / (dom_ms * 1e-3) / 1e9,
-                    "hbm_frac": bytes_launch / (dom_ms * 1e-3) / HBM_PEAK}
-        print(f"# roofline: error {err_ms:.4f} ms, update {upd_ms:.4f} ms per launch; {dom_name} at "
-              f"{achieved / 1e12:.1f} TFLOP/s = {100 * achieved / peak:.1f}% of peak, "
-              f"{bytes_launch / (dom_ms * 1e-3) / 1e9:.0f} GB/s algorithmic", file=sys.stderr, flush=True)
-    roofline.update(traffic_fields(sizes, B, cfg["dtype"]))
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        x_host = x.cpu().numpy()
-        cpu = cpu_baseline(cfg, W, b, x_host, args.cpu_budget)
-        print(f"# cpu baseline: {cpu['value']:.4g} sample-steps/s on {cpu['cores']} threads", file=sys.stderr,
-              flush=True)
-
-    rec = {
-        "metric": "relaxed samples*steps/sec at 1 GPU and % of MFMA/HBM roofline",
-        "value": value,
-        "unit": "sample-steps/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": cfg["dtype"],
-        "data": "synthetic (seeded random weights and inputs)",
-        "config": {"workload": f"{args.config}: {topology(sizes)} {ACT_NAME[cfg['act']]} "
-                               f"{cfg['dtype']}, B={B}, T={T}, eta={cfg['eta']}",
-                   "batch": B, "relax_steps": T, "layer_sizes": sizes, "parallelism": "single GPU"},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-    }
+    rec = bench_settle(args, args.config, cfg, args.steps, args.warmup, args.cpu_budget, pcie=True)
+    if args.config == "c5" and not args.no_extra:
+        # the configuration north_star's bf16 target is stated on, and the
+        # reference's own published workload, in the same line
+        rec["extra"] = {
+            "c3": bench_settle(args, "c3", CONFIGS["c3"], args.steps, min(args.warmup, 3), args.cpu_budget / 2),
+            "pub": bench_published(args),
+        }
     print(json.dumps(rec))
-    model.close()
 
 
 if __name__ == "__main__":

@@ -208,10 +208,13 @@ int pcd_pc_relax(pcd_model* model, const float* x0, int batch, int steps,
  * and the step loop runs as plain kernel launches (no cached graph).  A call
  * whose batch needs more scratch than that fails with PCD_INVALID_VALUE
  * before launching anything (pcd_last_error names the size).  Every call on a
- * device shares that device's array, so calls that overlap on one device
- * (other streams, other threads, other models) race and must be serialised by
- * the caller.  out_energy, when given, is written in place.  Asynchronous on
- * `stream`. */
+ * device shares that device's array: the library runs such calls one after
+ * another, whatever their streams, threads or models (each call's stream waits
+ * on an event the previous call recorded, set up with the array on the first
+ * call).  A call made while its stream is being captured into a graph is
+ * ordered only by that graph: the caller orders the graph's replays against
+ * other uses of the array.  out_energy, when given, is written in place.
+ * Asynchronous on `stream`. */
 int pcd_pc_relax_noalloc(pcd_model* model, const float* x0, int batch, int steps,
                          float* out_top, float* out_states, float* out_energy, void* stream);
 

@@ -295,9 +295,10 @@ class PcDeviceModel:
             raise ArgumentOutOfRangeException("inferenceSteps")
         hs = self.sizes[1:-1]
         if hidden is not None:
-            hidden = [np.ascontiguousarray(h, dtype=np.float32).reshape(B, s) for h, s in zip(hidden, hs)]
+            hidden = list(hidden)
             if len(hidden) != len(hs):
                 raise ArgumentException(f"hidden must hold {len(hs)} layers")
+            hidden = [np.ascontiguousarray(h, dtype=np.float32).reshape(B, s) for h, s in zip(hidden, hs)]
         dx, dl = DeviceTensor.from_host(x0), DeviceTensor.from_host(labels)
         en = DeviceTensor((B,))
         nh = B * sum(hs)

@@ -1241,11 +1241,15 @@ int pcd_event_elapsed_ms(float* ms, void* start, void* end) {
 // gives every CU a tile, then 128 x 128 while that does, else 64 x 64 (whose
 // few tiles split-K then spreads over the CUs); fp32 products with fewer
 // 64 x 64 tiles than CUs take the K-shared 32 x 32 tile.  `batch` products of
-// the same shape count together.
+// the same shape count together, but only among the tiles that fit one
+// product: a tile wider than the product (rounded up to 64) in either
+// dimension would be mostly padding, in MFMA work and in packed operand
+// memory, however many products there are.
 static Tile choose_gemm_tile(int dtype, int m, int n, int cus, int batch = 1) {
     auto tiles = [&](int t) { return (long)batch * ((m + t - 1) / t) * ((n + t - 1) / t); };
-    if (dtype != PCD_F32 && tiles(256) >= cus) return Tile{256, 256};
-    if (tiles(128) >= cus) return Tile{128, 128};
+    auto fits = [&](int t) { return t <= (int)round_up(m, 64) && t <= (int)round_up(n, 64); };
+    if (dtype != PCD_F32 && fits(256) && tiles(256) >= cus) return Tile{256, 256};
+    if (fits(128) && tiles(128) >= cus) return Tile{128, 128};
     if (dtype == PCD_F32 && tiles(64) < cus) return Tile{32, 32};
     return Tile{64, 64};
 }
@@ -1668,30 +1672,45 @@ int pcd_pc_relax(pcd_model* m, const float* x0, int batch, int steps, float* out
 // updates, energy partials, split-K partial tiles and counters), carved per
 // call.  Each device the library runs on holds its own copy of the array
 // until the process ends.  In host code the name is a host-side stand-in, not
-// a device address: host code uses only the address scratch_base() looks up.
+// a device address: host code uses only the address scratch_device() looks up.
 constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
 static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 
 namespace {
 
 constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
-char* g_scratch_base[kMaxScratchDevices] = {};
 
-// The device address of `scratch` on `device`, which must be current: looked
-// up with hipGetSymbolAddress on the first call for that device, then kept
-// (each device holds the array at its own address).
-int scratch_base(int device, char** out) {
+// One device's use of the array: its address, and the order of the calls
+// that use it.  `mu` is held for the whole of a call's enqueue, so calls from
+// several threads (and models) take the array one at a time on the host;
+// `done` is recorded on a call's stream after its last launch, and the next
+// call's stream waits on it before its first, so calls on different streams
+// also run one after another on the device, without any allocation.
+struct ScratchDevice {
+    std::mutex mu;
+    char* base = nullptr;
+    hipEvent_t done = nullptr;
+    bool recorded = false;
+};
+std::mutex g_scratch_mu;
+ScratchDevice g_scratch[kMaxScratchDevices];
+
+// The scratch record of `device`, which must be current.  Set up on the first
+// call for that device: the array's device address from hipGetSymbolAddress
+// (each device holds the array at its own address) and the ordering event.
+int scratch_device(int device, ScratchDevice** out) {
     if (device < 0 || device >= kMaxScratchDevices)
         return fail(PCD_INVALID_VALUE, "device %d beyond the %d the scratch table covers", device, kMaxScratchDevices);
     std::lock_guard<std::mutex> g(g_scratch_mu);
-    if (!g_scratch_base[device]) {
+    ScratchDevice& sd = g_scratch[device];
+    if (!sd.base) {
         void* p = nullptr;
         HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         if (!p) return fail(PCD_HIP_ERROR, "hipGetSymbolAddress(scratch) gave a null address");
-        g_scratch_base[device] = (char*)p;
+        HIP_TRY(hipEventCreateWithFlags(&sd.done, hipEventDisableTiming));
+        sd.base = (char*)p;
     }
-    *out = g_scratch_base[device];
+    *out = &sd;
     return PCD_SUCCESS;
 }
 
@@ -1750,8 +1769,18 @@ int pcd_pc_relax_noalloc(pcd_model* m, const float* x0, int batch, int steps, fl
     hipStream_t s = (hipStream_t)stream_;
     std::lock_guard<std::mutex> g(m->mu);
     HIP_TRY(hipSetDevice(m->device));
-    char* base = nullptr;
-    if (int st = scratch_base(m->device, &base)) return st;
+    ScratchDevice* sd = nullptr;
+    if (int st = scratch_device(m->device, &sd)) return st;
+    std::lock_guard<std::mutex> dg(sd->mu);
+    char* const base = sd->base;
+    // Outside graph capture, this call's work starts after the previous call's
+    // (on whatever stream) has finished with the array.  A call captured into
+    // a graph is ordered by the graph's own stream: the caller orders its
+    // replays against other uses of the array.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &cs));
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (!capturing && sd->recorded) HIP_TRY(hipStreamWaitEvent(s, sd->done, 0));
     const Tile tile = choose_tile(m, batch);
     Workspace w;
     w.stream = s;
@@ -1777,6 +1806,10 @@ int pcd_pc_relax_noalloc(pcd_model* m, const float* x0, int batch, int steps, fl
     if (int st = copy_out_rows(out_top, m->s[L - 1], w.M[L - 1], m->P[L - 1], batch, s)) return st;
     if (out_states)
         if (int st = copy_out_states(m, &w, out_states, batch, s)) return st;
+    if (!capturing) {
+        HIP_TRY(hipEventRecord(sd->done, s));
+        sd->recorded = true;
+    }
     return PCD_SUCCESS;
 }
 

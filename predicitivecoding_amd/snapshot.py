@@ -61,14 +61,32 @@ class GenerativeSnapshot:
                     "the batched forward would not reproduce the network's dynamics.")
         ws, bs = [], []
         for l in range(1, L):
-            w = np.ascontiguousarray(self.weights[l - 1], dtype=np.float32)
-            b = np.ascontiguousarray(self.biases[l - 1], dtype=np.float32).ravel()
+            # Own copies, read-only: the snapshot is immutable once made.  The
+            # drop-in uploads a snapshot's weights once and reuses the device
+            # copy on later calls, where the reference re-reads model.Weights
+            # on every call (BatchedPcForward.cs:62-64); an edit of the caller's
+            # arrays after construction therefore must not reach the snapshot,
+            # and an edit through the snapshot is refused (ValueError).
+            w = np.array(self.weights[l - 1], dtype=np.float32, order="C", copy=True)
+            b = np.array(self.biases[l - 1], dtype=np.float32, copy=True).ravel()
             if w.shape != (self.layer_sizes[l - 1], self.layer_sizes[l]):
                 raise ArgumentException(f"W_{l} has shape {w.shape}, expected "
                                         f"({self.layer_sizes[l - 1]}, {self.layer_sizes[l]})")
             if b.shape != (self.layer_sizes[l - 1],):
                 raise ArgumentException(f"b_{l} has shape {b.shape}, expected ({self.layer_sizes[l - 1]},)")
+            w.setflags(write=False)
+            b.setflags(write=False)
             ws.append(w)
             bs.append(b)
-        self.weights, self.biases = ws, bs
-        self.precisions = [float(p) for p in self.precisions]
+        self.weights, self.biases = tuple(ws), tuple(bs)
+        self.precisions = tuple(float(p) for p in self.precisions)
+        self.layer_sizes = tuple(self.layer_sizes)
+        object.__setattr__(self, "_frozen", True)
+
+    def __setattr__(self, name, value):
+        # Fields are set once, in __init__/__post_init__; a new model is a new
+        # snapshot (Network.ExportGenerativeSnapshot makes one per call).
+        if getattr(self, "_frozen", False):
+            raise NotSupportedException(f"GenerativeSnapshot is immutable: cannot set {name!r}; "
+                                        "export a new snapshot instead.")
+        object.__setattr__(self, name, value)

@@ -110,3 +110,30 @@ def test_clamped_classify_learn_argument_errors_without_gpu():
     assert L.pcd_pc_classify(None, None, 1, 1, None, None, None, None) == DeviceStatus.NotInitialized
     assert L.pcd_pc_learn(None, None, None, 1, 1, 0.01, 0.0, None, None) == DeviceStatus.NotInitialized
     assert L.pcd_pc_model_get_weights(None, 1, None, None) == DeviceStatus.NotInitialized
+
+
+def test_snapshot_is_an_immutable_copy():
+    # The drop-in uploads a snapshot's weights once and reuses the device copy
+    # (BatchedPcForward.cs:62-64 re-reads them per call instead): the snapshot
+    # therefore owns read-only copies.  Editing the caller's arrays afterwards
+    # does not reach it, editing through it is refused, and so is replacing a
+    # field.
+    from predicitivecoding_amd import GenerativeSnapshot
+    sizes = [6, 10, 4]
+    W = [np.ones((6, 10), np.float32), np.ones((10, 4), np.float32)]
+    b = [np.zeros(6, np.float32), np.zeros(10, np.float32)]
+    snap = GenerativeSnapshot(sizes, 1, 0.1, 0.0, False, W, b, [1.0, 1.0, 1.0])
+    assert snap.weights[0] is not W[0] and not np.shares_memory(snap.weights[0], W[0])
+    W[0][0, 0] = 5.0
+    b[1][3] = 2.0
+    assert snap.weights[0][0, 0] == 1.0 and snap.biases[1][3] == 0.0
+    with pytest.raises(ValueError):
+        snap.weights[0][0, 0] = 5.0
+    with pytest.raises(ValueError):
+        snap.biases[0][0] = 1.0
+    with pytest.raises(NotSupportedException):
+        snap.weights = [W[0] * 2, W[1]]
+    with pytest.raises(NotSupportedException):
+        snap.state_learning_rate = 0.5
+    with pytest.raises(TypeError):
+        snap.weights[0] = W[0]          # a tuple: the layer list cannot be edited either

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from oracle.pc_oracle import ACT
+from predicitivecoding_amd.errors import ArgumentException
 from tests.gpu_util import ROUND, build_case
 from tests.netgen import make_inputs, make_net, max_rel
 
@@ -268,6 +269,11 @@ def test_learn_from_hidden_states(oracle, dtype, tol):
     hidden = [(rng.standard_normal((7, s)) * 0.4).astype(np.float32) for s in sizes[1:-1]]
     m = _model(snap, dtype)
     try:
+        # one array too many (or too few) is refused before anything runs,
+        # not truncated to the hidden layer count
+        for wrong in (hidden + [hidden[0]], hidden[:1]):
+            with pytest.raises(ArgumentException):
+                m.learn(x, y, 9, 0.05, hidden=wrong)
         en, gh = m.learn(x, y, 9, 0.05, hidden=hidden, want_hidden=True)
         gw, gb = m.get_weights()
     finally:

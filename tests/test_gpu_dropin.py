@@ -117,3 +117,29 @@ def test_drop_in_releases_device_models_with_their_snapshots(oracle):
     del keep
     gc.collect()
     assert BatchedPcForward.cached_models() == base
+
+
+def test_drop_in_sees_the_snapshot_as_made(oracle):
+    # An in-place edit of the arrays a snapshot was made from, after its first
+    # call, must not leave the cached device model silently out of step with
+    # the snapshot: the snapshot holds its own read-only copies, so its
+    # weights (and the device model's) are the ones it was made with, and a
+    # new snapshot of the edited arrays settles with the edit.
+    from predicitivecoding_amd import BatchedPcForward, GenerativeSnapshot
+    W, b, P = make_net(SIZES, seed=61)
+    inputs = _inputs(4, seed=62)
+    x = np.stack(inputs)
+    snap = GenerativeSnapshot(SIZES, 1, 0.1, 0.0, False, W, b, list(P))
+    first = np.stack(BatchedPcForward.infer_get_top_batch(snap, inputs, 8))
+    W[0][:] *= 3.0                   # the caller edits its own arrays in place
+    with pytest.raises(ValueError):
+        snap.weights[0][0, 0] = 1.0  # and cannot edit the snapshot's
+    again = np.stack(BatchedPcForward.infer_get_top_batch(snap, inputs, 8))
+    assert np.array_equal(first, again)
+    ref, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, [w for w in snap.weights], list(snap.biases), P, x, 8)
+    assert max_rel(again, ref) < 1e-4
+    edited = GenerativeSnapshot(SIZES, 1, 0.1, 0.0, False, W, b, list(P))
+    new = np.stack(BatchedPcForward.infer_get_top_batch(edited, inputs, 8))
+    ref2, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, W, b, P, x, 8)
+    assert max_rel(new, ref2) < 1e-4
+    assert not np.allclose(new, first)

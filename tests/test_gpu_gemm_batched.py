@@ -11,7 +11,12 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(1, 1, 1, 1), (3, 37, 53, 29), (5, 64, 64, 64), (2, 200, 130, 333), (37, 8, 16, 8), (4, 512, 256, 384)]
+SHAPES = [(1, 1, 1, 1), (3, 37, 53, 29), (5, 64, 64, 64), (2, 200, 130, 333), (37, 8, 16, 8), (4, 512, 256, 384),
+          # many items: the tile is chosen from the item's own size (never larger
+          # than it), with the item count deciding among the tiles that fit --
+          # 64 x 64 for 512 small items, 128 x 128 (f32) and 256 x 256 (16-bit)
+          # when the items are that large and numerous enough to fill the CUs
+          (512, 64, 64, 64), (300, 128, 64, 128), (256, 256, 64, 256)]
 
 
 def _round(x, dtype):

@@ -95,3 +95,45 @@ def test_noalloc_refuses_a_batch_beyond_its_scratch():
         dx.free()
         top.free()
         model.close()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    # Two models' calls queued back to back on two streams, with no
+    # synchronisation between them, share the device's one scratch array: the
+    # library orders them (the second stream waits on the first call's event),
+    # so each result still equals pcd_pc_relax's bit for bit.
+    from predicitivecoding_amd import DeviceTensor, Stream
+    from predicitivecoding_amd._native import call
+    specs = [([1024, 2048, 1024, 64], 4, "bf16", 512, 9), ([784, 256, 256, 10], 1, "f32", 64, 7)]
+    models = [_model(sizes, act, dtype, 0, 0.05, seed=70 + i) for i, (sizes, act, dtype, _, _) in enumerate(specs)]
+    streams = [Stream(), Stream()]
+    bufs = []
+    try:
+        wants, outs = [], []
+        for (sizes, _, _, B, steps), model in zip(specs, models):
+            x = make_inputs(B, sizes[0], seed=B)
+            wants.append(_run("pcd_pc_relax", model, x, steps))
+            dx = DeviceTensor.from_host(x)
+            top = DeviceTensor.from_host(np.full((B, sizes[-1]), np.float32("nan"), np.float32))
+            states = DeviceTensor.from_host(np.full((B * sum(sizes),), np.float32("nan"), np.float32))
+            energy = DeviceTensor.from_host(np.full((steps, B), np.float32("nan"), np.float32))
+            bufs += [dx, top, states, energy]
+            outs.append((dx, top, states, energy))
+        for rep in range(3):
+            for (sizes, _, _, B, steps), model, stream, (dx, top, states, energy) in zip(specs, models, streams, outs):
+                call("pcd_pc_relax_noalloc", model.handle, dx.ptr, B, steps, top.ptr, states.ptr, energy.ptr,
+                     stream.handle)
+            for stream in streams:
+                stream.synchronize()
+            for i, (want, (_, top, states, energy)) in enumerate(zip(wants, outs)):
+                for what, g, w in zip(("top", "states", "energy"), (top.to_host(), states.to_host(),
+                                                                    energy.to_host()), want):
+                    assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), (rep, i, what)
+            print(f"two streams, round {rep}: both calls bit-identical to pcd_pc_relax", flush=True)
+    finally:
+        for t in bufs:
+            t.free()
+        for stream in streams:
+            stream.close()
+        for model in models:
+            model.close()
