@@ -927,6 +927,10 @@ bool run_persistent(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t 
     int nslots = 0;
     build_phase_sets(m, w, r.batch, r.tile, r.clamp_top, err, upd, &nslots);
     if (!persistent_fits(m, r.tile, err, upd)) return false;
+    // A caller capturing its stream into a graph gets the per-phase launches
+    // (this form waits for the settling, which a capture cannot).
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
     // workgroups of the launch: a multiple of the XCD count, all resident at once
     const int cap = persistent_blocks_per_cu() * m->cus / kXcds * kXcds;
     const int err_grid = phase_grid(err[0], m->tile_order), upd_grid = phase_grid(upd[0], m->tile_order);
