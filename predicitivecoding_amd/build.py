@@ -37,7 +37,14 @@ def _units():
         for bm, bn in TILES:
             units.append((INST_SOURCE, [f"-DPCD_OP_ID={op_id}", f"-DPCD_BM={bm}", f"-DPCD_BN={bn}"],
                           f"phase_{op}_{bm}x{bn}.o"))
+    units.extend(_direct_units())
     return units
+
+
+def _direct_units():
+    """The direct-weight 64 x 128 tile of the 16-bit operand types."""
+    return [(INST_SOURCE, [f"-DPCD_OP_ID={OPS[op]}", "-DPCD_BM=64", "-DPCD_BN=128", "-DPCD_WD=1"],
+             f"phase_{op}_64x128d.o") for op in ("bf16", "f16")]
 
 
 def _run(cmd):
@@ -61,6 +68,7 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> str:
                 raise RuntimeError(f"hipcc failed on {obj} ({rc}):\n{out}")
             if verbose and out.strip():
                 print(out)
+        check_direct_asm(hipcc, tmpdir, jobs)
         tmp = LIB + ".tmp"
         # -z defs: a tile the host dispatches but no unit instantiates fails here,
         # not when the library is loaded
@@ -70,6 +78,28 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> str:
             raise RuntimeError(f"link failed ({rc}):\n{out}")
     os.replace(tmp, LIB)
     return LIB
+
+
+def check_direct_asm(hipcc: str, tmpdir: str, jobs: int) -> None:
+    """Compile the direct-weight units to device assembly and check their inline-asm loads' waits."""
+    from predicitivecoding_amd.asm_check import check_asm
+
+    units = _direct_units()
+    cmds = [[hipcc, *HIPCC_FLAGS, *flags, "--offload-device-only", "-S", src,
+             "-o", os.path.join(tmpdir, obj.replace(".o", ".s"))] for src, flags, obj in units]
+    with ThreadPoolExecutor(jobs) as ex:
+        results = list(ex.map(_run, cmds))
+    for (src, flags, obj), (rc, out) in zip(units, results):
+        if rc != 0:
+            raise RuntimeError(f"hipcc -S failed on {obj} ({rc}):\n{out}")
+        with open(os.path.join(tmpdir, obj.replace(".o", ".s"))) as f:
+            found = check_asm(f.read())
+        if not found:
+            raise RuntimeError(f"{obj}: no phase kernel in the device assembly")
+        bad = {k: v for k, v in found.items() if v}
+        if bad:
+            lines = [f"  {k}: {v[0]} (+{len(v) - 1} more)" for k, v in bad.items()]
+            raise RuntimeError(f"{obj}: inline-asm loads read or overwritten in flight:\n" + "\n".join(lines))
 
 
 def build_oracle() -> str | None:

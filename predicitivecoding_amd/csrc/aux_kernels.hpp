@@ -60,6 +60,24 @@ __global__ void pack_kernel(const void* __restrict__ src, int src_is_f32, int ro
     }
 }
 
+// Fragment-major copy of a 16-bit operand [rows x cols] with rows `ld`
+// elements apart (rows a multiple of 32, cols of 16): the 16-byte unit at
+// dst[(rb * cols/16 + kc) * 64 + lane] holds row rb*32 + lane%32, elements
+// kc*16 + 8*(lane/32) .. +7, i.e. lane `lane`'s operand of a 32 x 32 x 16
+// MFMA over rows rb*32.. and K chunk kc.  A wave then reads one fragment as
+// 1 KB of contiguous memory.
+__global__ void frag_pack_kernel(const u32x4* __restrict__ src, int ld, int rows, int cols, u32x4* __restrict__ dst) {
+    const int kcs = cols / 16;
+    const size_t n = (size_t)(rows / 32) * kcs * 64;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i % 64);
+        const size_t f = i / 64;
+        const int kc = (int)(f % kcs), rb = (int)(f / kcs);
+        const int r = rb * 32 + lane % 32;
+        dst[i] = src[((size_t)r * ld + (size_t)kc * 16 + 8 * (lane / 32)) / 8];
+    }
+}
+
 // pack_kernel over `batch` matrices stored back to back: item i of src is the
 // [rows x cols] matrix (or [cols x rows] read transposed) at src + i * rows *
 // cols, packed into the zero-padded [prow x pcol] buffer at dst + i * prow *

@@ -360,7 +360,13 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
 #ifndef PCD_KSW_OCC
 #define PCD_KSW_OCC 3
 #endif
-template <int BM, int BN, int OPB = 4> struct TileCfg {
+#ifndef PCD_WD_NS
+#define PCD_WD_NS 5    // direct-weight tile: 40 KB ring (4 stages of lead), three workgroups per CU
+#endif
+#ifndef PCD_WD_OCC
+#define PCD_WD_OCC 3
+#endif
+template <int BM, int BN, int OPB = 4, bool WDIR = false> struct TileCfg {
     // 256 x 256 runs 8 waves (2 x 4 of 128 x 64: two waves per SIMD share the
     // MFMA pipe) over 128-byte K stages, double buffered (128 KB of LDS, one
     // workgroup per CU).  The other tiles run 4 waves (2 x 2) with rings of at
@@ -375,8 +381,17 @@ template <int BM, int BN, int OPB = 4> struct TileCfg {
     // a quarter of the MFMA issue time of a 64 x 64 tile's.  The waves' sums
     // meet in LDS after the loop.
     static constexpr bool KSW = BM == 32 && BN == 32;
+    static constexpr bool WD = WDIR;
+    // WD (direct weights, 64 x 128 on 16-bit operands only): the weight
+    // operand is read from a fragment-major copy straight into registers
+    // (each wave's 1 KB fragment of a 16-deep K chunk is one contiguous,
+    // non-temporal 16-byte-per-lane load) and only the batch rows go through
+    // LDS.  Each of the 4 waves owns all 64 rows and 32 columns, so no two
+    // waves read the same weights.  The small-batch settlings, which stream
+    // every weight once per phase, are bound by that stream.
+    static_assert(!WDIR || (BM == 64 && BN == 128 && OPB == 2), "direct weights: 64 x 128 tiles of 16-bit operands");
     static constexpr int KW = KSW ? 4 : 1;                 // waves sharing one block's K
-    static constexpr int WM = KSW ? 1 : 2, WN = BIG ? 4 : KSW ? 1 : 2;
+    static constexpr int WM = (KSW || WD) ? 1 : 2, WN = (BIG || WD) ? 4 : KSW ? 1 : 2;
     static constexpr int NWAVES = WM * WN * KW, NT = 64 * NWAVES;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -385,23 +400,28 @@ template <int BM, int BN, int OPB = 4> struct TileCfg {
     static constexpr int UNITS = RB / 16;                  // 16-byte units per row
     static constexpr int NC = RB / 32;                     // 32-byte MFMA chunks per stage
     static constexpr int NCW = NC / KW;                    // chunks of a stage one wave takes
-    static constexpr int stage_bytes = (BM + BN) * RB;
-    static constexpr int NS_WANT = BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : KSW ? PCD_KSW_NS : (BM + BN >= 320) ? 3 : PCD_SMALL_NS;
-    static constexpr int NS = BIG ? NS_WANT : (NS_WANT * stage_bytes <= 80 * 1024 ? NS_WANT : 80 * 1024 / stage_bytes);   // stages in the LDS ring
+    static constexpr int LDS_ROWS = WD ? BM : BM + BN;     // operand rows a stage holds in LDS
+    static constexpr int stage_bytes = LDS_ROWS * RB;
+    static constexpr int NS_WANT = WD ? PCD_WD_NS : BIG ? PCD_BIG_NS : MID ? PCD_MID_NS : KSW ? PCD_KSW_NS : (BM + BN >= 320) ? 3 : PCD_SMALL_NS;
+    static constexpr int NS = (BIG || WD) ? NS_WANT : (NS_WANT * stage_bytes <= 80 * 1024 ? NS_WANT : 80 * 1024 / stage_bytes);   // stages in the LDS ring
     static constexpr int D = NS - 1;                       // prefetch distance (stages)
-    static constexpr int OCC = BIG ? 1 : KSW ? PCD_KSW_OCC : PCD_OCC_SMALL;   // workgroups per CU the registers are sized for
+    static constexpr int OCC = BIG ? 1 : KSW ? PCD_KSW_OCC : WD ? PCD_WD_OCC : PCD_OCC_SMALL;   // workgroups per CU the registers are sized for
     static constexpr int ROWS_PER_LOAD = 64 * 16 / RB;     // rows one wave-wide 16-byte-per-lane load fills
-    static constexpr int QPW = (BM + BN) / ROWS_PER_LOAD / NWAVES;   // loads per wave per stage
+    static constexpr int QPW = LDS_ROWS / ROWS_PER_LOAD / NWAVES;   // loads per wave per stage
+    // vector-memory operations a wave issues per stage (DMA, then weights)
+    static constexpr int VPS = QPW + (WD ? NCW : 0);
     static_assert(FM >= 1 && FN >= 1 && QPW >= 1, "tile too small");
-    static_assert((BM + BN) % (NWAVES * ROWS_PER_LOAD) == 0, "stage rows must split evenly over the waves");
+    static_assert(LDS_ROWS % (NWAVES * ROWS_PER_LOAD) == 0, "stage rows must split evenly over the waves");
     static_assert(NCW % 2 == 0 || NCW == 1, "fragment buffers alternate within a stage (or per stage)");
-    static_assert(D >= 1 && D * QPW < 64, "stage_ready waits on at most 63 loads");
+    static_assert(D >= 1 && D * VPS < 64, "stage_ready waits on at most 63 loads");
     static_assert(NS * stage_bytes <= 160 * 1024, "LDS ring exceeds the 160 KB of a CU");
     static_assert(64 % (RB / OPB) == 0, "K is padded to 64 elements: a stage's K must divide it");
 };
 
 // Energy partial slots one tile column owns (one per wave column).
-template <int BM, int BN> constexpr int energy_slots_per_tile_n() { return TileCfg<BM, BN>::WN; }
+template <int BM, int BN, bool WD = false> constexpr int energy_slots_per_tile_n() {
+    return TileCfg<BM, BN, WD ? 2 : 4, WD>::WN;
+}
 
 // Direct global -> LDS copy of 16 bytes per lane (gfx950 global_load_lds_dwordx4):
 // lane l's bytes land at LDS address m0 + 16 l.  Issued as inline asm so the
@@ -411,6 +431,27 @@ template <int BM, int BN> constexpr int energy_slots_per_tile_n() { return TileC
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) {
         asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_addr) : "memory", "m0");
+}
+
+// Non-temporal 16-byte load per lane into registers, issued as inline asm so
+// that the compiler does not wait for it before the next loads.  The compiler
+// does not know the registers are still being written: the kernel waits for
+// the load itself (wait_vmcnt_pin) before it reads them, and keeps them
+// allocated (pin_regs) until every such load has landed, so no other value
+// is placed in them meanwhile.
+__device__ __forceinline__ u32x4 gload_nt16(const void* gaddr) {
+    u32x4 r;
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(r) : "v"(gaddr) : "memory");
+    return r;
+}
+// s_waitcnt vmcnt(N); the four registers are its operands, so the code that
+// reads them stays after it.
+template <int N> __device__ __forceinline__ void wait_vmcnt_pin(u32x4 (&w)[4]) {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]) : "n"(N) : "memory");
+}
+__device__ __forceinline__ void pin_regs(u32x4 (&w)[4]) {
+    asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]));
 }
 #pragma clang diagnostic pop
 
@@ -687,8 +728,8 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
 // LDS of one phase unit: the stage ring, which after the main loop the
 // settling epilogues reuse as two store-staging regions per wave and the
 // tile's bias.
-template <typename OP, int BM, int BN> constexpr int phase_smem_bytes() {
-    using C = TileCfg<BM, BN, OpTraits<OP>::bytes>;
+template <typename OP, int BM, int BN, bool WD = false> constexpr int phase_smem_bytes() {
+    using C = TileCfg<BM, BN, OpTraits<OP>::bytes, WD>;
     // The K-shared tile's tail needs its reduce-scatter, the row energies and a
     // flag; the others two store-staging regions per wave and the bias.
     constexpr int STAGE_END = C::KSW ? C::KW * 16 * 64 * 4 + C::KW * 32 * 4 + 16 : 2 * C::NWAVES * kStageWaveBytes + BN * 4;
@@ -701,11 +742,11 @@ template <typename OP, int BM, int BN> constexpr int phase_smem_bytes() {
 // persistent launch runs every virtual block of a phase, several per
 // workgroup, between grid barriers.  `smem` is the workgroup's LDS of
 // phase_smem_bytes() bytes.
-template <typename OP, int BM, int BN, int EPI>
+template <typename OP, int BM, int BN, int EPI, bool WD = false>
 __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, const PhaseArgs& args, const int vblock,
                                            const int vgrid, char* smem) {
     constexpr int OPB = OpTraits<OP>::bytes;
-    using C = TileCfg<BM, BN, OPB>;
+    using C = TileCfg<BM, BN, OPB, WD>;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -846,15 +887,96 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // others find the line resident, instead of all of them waiting on the same
     // miss.  The sum over K is taken in that rotated order, so a row's result
     // depends on the row tile it falls in (still the same run to run).
-    const int koff = (args.k_stagger > 1 && nk > 0) ? ((tm + tn) % args.k_stagger) % nk : 0;
+    const int koff = (!C::WD && args.k_stagger > 1 && nk > 0) ? ((tm + tn) % args.k_stagger) % nk : 0;
     const char* Ag = (const char*)P.A + (size_t)row0 * P.lda * OPB + (size_t)kb * C::RB;
     const char* Bg = (const char*)P.B + (size_t)col0 * P.ldb * OPB + (size_t)kb * C::RB;
     const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
 
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+    const int half = lane >> 5, lr = lane & 31;
+    // The settling epilogues (error, update) take each block transposed: the
+    // B-side fragment goes in as the MFMA's first operand, so a lane holds one
+    // row and runs of four consecutive columns, which those epilogues read and
+    // write 16 bytes at a time.
+    constexpr bool TRM = EPI == EPI_ERROR || EPI == EPI_UPDATE;
+    if constexpr (C::WD) {
+        // ---- direct-weight main loop.  Per stage, each wave DMAs its QPW
+        // loads of the batch rows into the LDS ring and loads its NCW weight
+        // fragments (one per 16-deep K chunk, 1 KB contiguous in the
+        // fragment-major copy) into a ring of D register sets.  Stage kt's
+        // DMA and weights are issued D stages ahead, DMA first, so waiting
+        // until at most (D - 1) * VPS vector-memory operations are in flight
+        // retires both; the barrier after the wait publishes every wave's
+        // DMA.  Loads past the last stage repeat the last one (in bounds,
+        // never read), so every stage issues the same count.  No K stagger:
+        // the weight streams of a phase never share rows.
+        const size_t kc16 = (size_t)P.K / 16;   // 16-deep K chunks of a weight row
+        const char* wsrc = (const char*)P.B + (((size_t)(col0 / 32 + wn) * kc16 + (size_t)kb * C::NCW) * 64 + lane) * 16;
+        const char* asrc[C::QPW];
+#pragma unroll
+        for (int i = 0; i < C::QPW; ++i) {
+            const int R = (wave_u * C::QPW + i) * C::ROWS_PER_LOAD + lane / C::UNITS;
+            asrc[i] = Ag + (size_t)R * lda_b + swz<C::RB>(R, lane % C::UNITS) * 16;
+        }
+        auto issue_a = [&](int kt) PCD_INLINE {
+            const int kk = min(kt, nk - 1);
+            const uint32_t base = lds0 + (kt % C::NS) * C::stage_bytes + wave_u * C::QPW * 1024;
+#pragma unroll
+            for (int i = 0; i < C::QPW; ++i) lds_dma16(asrc[i] + (size_t)kk * C::RB, base + i * 1024);
+        };
+        auto issue_w = [&](int kt, u32x4 (&w)[C::NCW]) PCD_INLINE {
+            const char* src = wsrc + (size_t)min(kt, nk - 1) * (C::NCW * 1024);
+            static_for<0, C::NCW>([&](auto Cc) PCD_INLINE { w[Cc] = gload_nt16(src + decltype(Cc)::value * 1024); });
+        };
+        static_assert(C::NCW == 4 && C::FN == 1, "the direct-weight ring holds four chunks of one block column");
+        u32x4 wr[C::D][C::NCW];
+        static_for<0, C::D>([&](auto J) PCD_INLINE {
+            issue_a(decltype(J)::value);
+            issue_w(decltype(J)::value, wr[decltype(J)::value]);
+        });
+        // Whole groups of D stages: every stage slot of a group waits, DMAs and
+        // refills (the same vector-memory sequence on every path, which the
+        // fixed wait counts rely on); slots past the last stage skip only the
+        // LDS reads and MFMAs.
+        for (int kt0 = 0; kt0 < nk; kt0 += C::D) {
+            static_for<0, C::D>([&](auto J) PCD_INLINE {
+                constexpr int j = decltype(J)::value;
+                const int kt = kt0 + j;
+                wait_vmcnt_pin<(C::D - 1) * C::VPS>(wr[j]);
+                __syncthreads();
+                issue_a(kt + C::D);
+                if (kt < nk) {
+                    const char* st = smem + (kt % C::NS) * C::stage_bytes;
+                    u32x4 fa[C::NCW][C::FM];
+                    static_for<0, C::NCW>([&](auto Cc) PCD_INLINE {
+                        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+                            constexpr int c = decltype(Cc)::value, i = decltype(I)::value;
+                            const int R = i * 32 + lr;
+                            fa[c][i] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
+                        });
+                    });
+                    static_for<0, C::NCW>([&](auto Cc) PCD_INLINE {
+                        static_for<0, C::FM>([&](auto I) PCD_INLINE {
+                            constexpr int c = decltype(Cc)::value, i = decltype(I)::value;
+                            if constexpr (TRM) mfma_chunk<OP>(accs[0][i][0], wr[j][c], fa[c][i]);
+                            else mfma_chunk<OP>(accs[0][i][0], fa[c][i], wr[j][c]);
+                        });
+                    });
+                }
+                __builtin_amdgcn_sched_barrier(0);   // the refill follows the MFMAs that read the set
+                issue_w(kt + C::D, wr[j]);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+        // The last D sets are never read: their loads land before anything
+        // else may take their registers.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        static_for<0, C::D>([&](auto J) PCD_INLINE { pin_regs(wr[decltype(J)::value]); });
+    } else {
     // This lane's source of each of its wave's QPW loads per stage: combined
     // stage row R = q*ROWS_PER_LOAD + lane/UNITS (A rows, then B rows),
     // physical unit lane%UNITS, which holds logical unit swz(R, lane%UNITS).
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const char* src[C::QPW];
 #pragma unroll
     for (int i = 0; i < C::QPW; ++i) {
@@ -863,7 +985,6 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         const int unit = swz<C::RB>(R, lane % C::UNITS);
         src[i] = R < BM ? Ag + (size_t)R * lda_b + unit * 16 : Bg + (size_t)(R - BM) * ldb_b + unit * 16;
     }
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
     auto issue_stage = [&](int kt) PCD_INLINE {
         const uint32_t base = lds0 + (kt % C::NS) * C::stage_bytes + wave_u * C::QPW * 1024;
         int kk = kt + koff;
@@ -872,7 +993,6 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         for (int i = 0; i < C::QPW; ++i) lds_dma16(src[i] + (size_t)kk * C::RB, base + i * 1024);
     };
     // Fragments of K chunk c (32 bytes per row) of the stage in `slot`.
-    const int half = lane >> 5, lr = lane & 31;
     auto read_frags = [&](int slot, int c, u32x4* a, u32x4* b) PCD_INLINE {
         const char* st = smem + slot * C::stage_bytes;
 #pragma unroll
@@ -886,11 +1006,6 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             b[j] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
         }
     };
-    // The settling epilogues (error, update) take each block transposed: the
-    // B-side fragment goes in as the MFMA's first operand, so a lane holds one
-    // row and runs of four consecutive columns, which those epilogues read and
-    // write 16 bytes at a time.
-    constexpr bool TRM = EPI == EPI_ERROR || EPI == EPI_UPDATE;
     auto mfmas = [&](const u32x4* a, const u32x4* b) PCD_INLINE {
         if constexpr (F32OP) {
             // K component s of every block before component s + 1 of any.
@@ -975,6 +1090,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         if constexpr (c + 1 < NC) read_frags((nk - 1) % C::NS, c0 + c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
         mfmas(fa[c & 1], fb[c & 1]);
     });
+    }   // LDS-operand main loop
     static_for<1, NSPLIT>([&](auto Kc) PCD_INLINE {
 #pragma unroll
         for (int i = 0; i < C::FM; ++i)
@@ -1359,12 +1475,13 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
 // kernel argument, so it sits at offset 0 of the kernarg segment: the problems
 // are indexed there (scalar loads from constant memory) instead of being
 // copied to scratch.
-template <typename OP, int BM, int BN, int EPI>
-__global__ void __launch_bounds__((TileCfg<BM, BN>::NT), (TileCfg<BM, BN>::OCC))
+template <typename OP, int BM, int BN, int EPI, bool WD = false>
+__global__ void __launch_bounds__((TileCfg<BM, BN, OpTraits<OP>::bytes, WD>::NT),
+                                  (TileCfg<BM, BN, OpTraits<OP>::bytes, WD>::OCC))
 phase_kernel(const ProblemSet set, const PhaseArgs args) {
-    __shared__ __attribute__((aligned(16))) char smem[phase_smem_bytes<OP, BM, BN>()];
-    phase_unit<OP, BM, BN, EPI>((KProblem*)__builtin_amdgcn_kernarg_segment_ptr(), set.n, args, blockIdx.x, gridDim.x,
-                                smem);
+    __shared__ __attribute__((aligned(16))) char smem[phase_smem_bytes<OP, BM, BN, WD>()];
+    phase_unit<OP, BM, BN, EPI, WD>((KProblem*)__builtin_amdgcn_kernarg_segment_ptr(), set.n, args, blockIdx.x,
+                                    gridDim.x, smem);
 }
 
 // ------------------------------------------------------- persistent settling

@@ -165,9 +165,13 @@ int launch_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid,
 }
 
 // GEMM tile shapes compiled into the library (rows x columns of the output).
+// wd: the direct-weight 64 x 128 tile of the 16-bit settlings, whose weight
+// operand is the model's fragment-major copy (never chosen by the caller).
 struct Tile {
     int m, n;
+    bool wd = false;
 };
+bool same_tile(Tile a, Tile b) { return a.m == b.m && a.n == b.n && a.wd == b.wd; }
 bool tile_supported(Tile t) {
     return (t.m == 32 && t.n == 32) || (t.m == 64 && (t.n == 64 || t.n == 128 || t.n == 256)) ||
            (t.m == 128 && t.n == 128) || (t.m == 256 && t.n == 128) || (t.m == 256 && t.n == 256);
@@ -175,6 +179,10 @@ bool tile_supported(Tile t) {
 
 template <typename OP>
 int launch_op(Tile tile, int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t s) {
+    if (tile.wd) {
+        if constexpr (std::is_same<OP, float>::value) return fail(PCD_INVALID_VALUE, "direct-weight tile on fp32");
+        else return from_hip(launch_phase_tile<OP, 64, 128, true>(epi, set, args, grid, s), "phase_kernel launch");
+    }
     if (tile.m == 32 && tile.n == 32) return launch_tile<OP, 32, 32>(epi, set, args, grid, s);
     if (tile.m == 64 && tile.n == 64) return launch_tile<OP, 64, 64>(epi, set, args, grid, s);
     if (tile.m == 64 && tile.n == 128) return launch_tile<OP, 64, 128>(epi, set, args, grid, s);
@@ -350,6 +358,10 @@ struct pcd_model {
     std::vector<float> prec;
     std::vector<void*> W, WT;           // [L] operand type; W[l] is [R(s_{l-1}) x P_l], WT[l] [R(s_l) x P_{l-1}]
     std::vector<float*> W32;            // [L] fp32 master weights of 16-bit models, laid out as W[l]
+    // [L] fragment-major copies of W[l] and WT[l] (frag_pack_kernel), kept for
+    // 16-bit models whose small-batch settlings take the direct-weight tile
+    // (direct_eligible); refreshed wherever W[l] and WT[l] change
+    std::vector<void*> Wpk, WTpk;
     std::vector<float*> bias;           // [L] fp32 [P_{l-1}]
     std::mutex mu;
     std::vector<std::unique_ptr<Workspace>> ws;
@@ -362,6 +374,7 @@ struct pcd_model {
     int k_stagger = 0;                  // settling phases: kKStaggerAuto (16-bit default), 0 off, or a fixed value
     int ragged_tiles = 1;               // ragged phases deal only the row tiles still running
     int ragged_order = 1;               // ragged requests settle in decreasing step budget (0: caller's order)
+    int direct = 1;                     // direct-weight tile: 0 never, 1 where direct_eligible, 2 every batch <= 64 rows
     float prof_err_ms = 0.f, prof_upd_ms = 0.f;
     int prof_launches = 0;
     uint64_t clock = 0;
@@ -388,6 +401,45 @@ int dev_alloc_zero(std::vector<void*>& owned, void** out, size_t bytes) {
     return PCD_SUCCESS;
 }
 
+// Fragment-major copies of layer l's operand-type weights (W[l] and WT[l]),
+// for models that keep them; enqueued on s after whatever wrote W[l] and WT[l].
+int repack_direct(pcd_model* m, int l, hipStream_t s) {
+    if (m->Wpk.empty() || !m->Wpk[l]) return PCD_SUCCESS;
+    const int Rlo = (int)round_up(m->s[l - 1], kRowPad), Rsz = (int)round_up(m->s[l], kRowPad);
+    const int g1 = (int)std::min<size_t>(((size_t)Rlo * m->P[l] / 8 + 255) / 256, 8192);
+    const int g2 = (int)std::min<size_t>(((size_t)Rsz * m->P[l - 1] / 8 + 255) / 256, 8192);
+    hipLaunchKernelGGL(frag_pack_kernel, dim3(g1), dim3(256), 0, s, (const u32x4*)m->W[l], m->P[l], Rlo, m->P[l],
+                       (u32x4*)m->Wpk[l]);
+    hipLaunchKernelGGL(frag_pack_kernel, dim3(g2), dim3(256), 0, s, (const u32x4*)m->WT[l], m->P[l - 1], Rsz,
+                       m->P[l - 1], (u32x4*)m->WTpk[l]);
+    return from_hip(hipGetLastError(), "frag_pack_kernel launch");
+}
+
+// Allocates and fills the fragment-major weight copies of a 16-bit model
+// that does not keep them (the option that forces the direct-weight tile).
+int alloc_direct(pcd_model* m) {
+    HIP_TRY(hipDeviceSynchronize());   // the weights may still be written by queued work
+    std::vector<void*> owned;
+    std::vector<void*> wpk(m->L, nullptr), wtpk(m->L, nullptr);
+    int st = PCD_SUCCESS;
+    for (int l = 1; l < m->L && !st; ++l) {
+        const size_t rlo = round_up(m->s[l - 1], kRowPad), rsz = round_up(m->s[l], kRowPad);
+        st = dev_alloc_zero(owned, &wpk[l], rlo * m->P[l] * 2);
+        if (!st) st = dev_alloc_zero(owned, &wtpk[l], rsz * m->P[l - 1] * 2);
+    }
+    if (!st) {
+        m->Wpk = wpk;
+        m->WTpk = wtpk;
+        for (int l = 1; l < m->L && !st; ++l) st = repack_direct(m, l, 0);
+        if (!st) st = from_hip(hipDeviceSynchronize(), "direct-weight copies");
+        if (!st) return PCD_SUCCESS;
+        m->Wpk.clear();
+        m->WTpk.clear();
+    }
+    for (void* p : owned) (void)hipFree(p);
+    return st;
+}
+
 // Tiles of one error phase at `batch` rows.
 long error_phase_tiles(const pcd_model* m, int batch, Tile t) {
     long tiles = 0;
@@ -407,11 +459,15 @@ long error_phase_tiles(const pcd_model* m, int batch, Tile t) {
 // fp32 persistent form, built on 64 x 64, is asked for.
 Tile choose_tile(const pcd_model* m, int batch) {
     if (m->tile_m > 0) return Tile{m->tile_m, m->tile_n};
+    const bool have_direct = m->direct && !m->Wpk.empty() && m->Wpk[1];
+    if (m->direct == 2 && have_direct && batch <= 64) return Tile{64, 128, true};   // forced (option)
     if (!(m->dtype == PCD_F32 && m->persistent) && error_phase_tiles(m, batch, Tile{64, 64}) < m->cus)
         return Tile{32, 32};
     // A batch that fits one 64-row tile: any taller tile is mostly padding rows
-    // (its MFMAs and its state loads wasted), and the phases stream weights.
-    if (batch <= 64) return Tile{64, 64};
+    // (its MFMAs and its state loads wasted), and the phases stream weights,
+    // which the direct-weight tile streams fastest (c5's network at 64 rows:
+    // the weights at 5.8 TB/s in its main loop against 5.0 for 64 x 64).
+    if (batch <= 64) return have_direct ? Tile{64, 128, true} : Tile{64, 64};
     const long want = 2L * m->cus;
     if (m->dtype != PCD_F32) {
         bool wide = true;
@@ -422,8 +478,18 @@ Tile choose_tile(const pcd_model* m, int batch) {
     return Tile{64, 64};
 }
 
+// Whether a 16-bit model keeps fragment-major weight copies for the
+// direct-weight tile: its batches of up to 64 rows run 64 x 64 tiles otherwise
+// (not the K-shared 32 x 32), and its error phase has at least one
+// direct-weight tile per CU.
+bool direct_eligible(const pcd_model* m) {
+    return m->dtype != PCD_F32 && error_phase_tiles(m, 64, Tile{64, 64}) >= m->cus &&
+           error_phase_tiles(m, 64, Tile{64, 128, true}) >= m->cus;
+}
+
 // Energy partial slots a tile column owns: one per wave column of the tile.
 int slots_per_tile_n(Tile t) {
+    if (t.wd) return energy_slots_per_tile_n<64, 128, true>();
     if (t.m == 32 && t.n == 32) return energy_slots_per_tile_n<32, 32>();
     if (t.m == 256 && t.n == 256) return energy_slots_per_tile_n<256, 256>();
     if (t.m == 256 && t.n == 128) return energy_slots_per_tile_n<256, 128>();
@@ -442,7 +508,7 @@ int energy_slots(const pcd_model* m, Tile tile) {
 
 // The most slots any supported tile needs (sizes the workspace once).
 int max_energy_slots(const pcd_model* m) {
-    const Tile tiles[] = {{32, 32}, {64, 64}, {64, 128}, {64, 256}, {128, 128}, {256, 128}, {256, 256}};
+    const Tile tiles[] = {{32, 32}, {64, 64}, {64, 128}, {64, 256}, {128, 128}, {256, 128}, {256, 256}, {64, 128, true}};
     int slots = 0;
     for (Tile t : tiles) slots = std::max(slots, energy_slots(m, t));
     return slots;
@@ -460,7 +526,7 @@ size_t split_count_bytes(const pcd_model* m) { return round_up((size_t)split_par
 
 
 int split_factor(int cus, int split_k, long tiles, Tile tile) {
-    if (!split_k || tile.m * tile.n > 128 * 128 || tiles < 1 || tiles * 2 > cus) return 1;
+    if (!split_k || tile.wd || tile.m * tile.n > 128 * 128 || tiles < 1 || tiles * 2 > cus) return 1;
     return (int)std::min<long>(kMaxSplit, cus / tiles);
 }
 
@@ -506,7 +572,7 @@ void assign_split(int cus, int split_k, int dtype, Tile tile, const SplitScratch
     auto wanted = [&](const Problem& p) {
         const int t = p.tiles_m * p.tiles_n;
         const int share = (t + kXcds - 1) / kXcds;
-        const int fb = (split_k && small_tile && share < per_xcd) ? per_xcd / share : 1;
+        const int fb = (split_k && small_tile && !tile.wd && share < per_xcd) ? per_xcd / share : 1;
         return std::max(1, std::min({std::max(f, fb), kMaxSplit, p.K / stage_k(dtype, tile) / min_stages}));
     };
     // All or nothing: a phase whose splits do not all fit the scratch splits
@@ -609,7 +675,7 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         std::memset(&p, 0, sizeof p);
         p.A = state_operand(m, w, l);
         p.lda = m->P[l];
-        p.B = m->W[l];
+        p.B = tile.wd ? m->Wpk[l] : m->W[l];
         p.ldb = m->P[l];
         p.M = batch;
         p.N = m->s[l - 1];
@@ -634,7 +700,7 @@ void build_phase_sets(const pcd_model* m, const Workspace* w, int batch, Tile ti
         std::memset(&p, 0, sizeof p);
         p.A = w->D[l];
         p.lda = m->P[l - 1];
-        p.B = m->WT[l];
+        p.B = tile.wd ? m->WTpk[l] : m->WT[l];
         p.ldb = m->P[l - 1];
         p.M = batch;
         p.N = m->s[l];
@@ -769,7 +835,7 @@ int enqueue_relax(pcd_model* m, Workspace* w, const RelaxSpec& r, hipStream_t s,
             Problem& p = ps.p[0];
             p.A = state_operand(m, w, l);
             p.lda = m->P[l];
-            p.B = m->W[l];
+            p.B = tile.wd ? m->Wpk[l] : m->W[l];
             p.ldb = m->P[l];
             p.M = batch;
             p.N = m->s[l - 1];
@@ -854,8 +920,7 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
     const int requests = r.row_req ? r.requests : 0;
     for (auto& p : w->plans)
         if (p->batch == r.batch && p->steps == r.steps && p->want_energy == want_energy &&
-            p->clamp_top == r.clamp_top && p->keep_hidden == r.keep_hidden && p->tile.m == r.tile.m &&
-            p->tile.n == r.tile.n &&
+            p->clamp_top == r.clamp_top && p->keep_hidden == r.keep_hidden && same_tile(p->tile, r.tile) &&
             p->requests == requests && (requests == 0 || (p->exit_rule == r.exit_rule &&
                                                           std::memcmp(&p->exit_thr, &r.exit_thr, 4) == 0))) {
             p->last_use = ++m->clock;
@@ -1491,6 +1556,10 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
     const int ob = op_bytes(dtype);
     std::vector<void*> owned;
     auto cleanup = [&]() { for (void* p : owned) (void)hipFree(p); };
+    if (direct_eligible(m.get())) {
+        m->Wpk.assign(levels, nullptr);
+        m->WTpk.assign(levels, nullptr);
+    }
     for (int l = 1; l < levels; ++l) {
         const int lo = sizes[l - 1], sz = sizes[l];
         const int Rlo = (int)round_up(lo, kRowPad), Rsz = (int)round_up(sz, kRowPad);
@@ -1505,6 +1574,13 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
         m->W[l] = w;
         m->WT[l] = wt;
         m->bias[l] = (float*)bb;
+        if (!m->Wpk.empty()) {
+            if ((st = dev_alloc_zero(owned, &m->Wpk[l], (size_t)Rlo * m->P[l] * ob)) ||
+                (st = dev_alloc_zero(owned, &m->WTpk[l], (size_t)Rsz * m->P[l - 1] * ob))) {
+                cleanup();
+                return st;
+            }
+        }
         if (dtype != PCD_F32) {
             // fp32 masters, which the learning step updates (Network.LearnMixed's scheme)
             void* w32 = nullptr;
@@ -1543,6 +1619,7 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
             hipLaunchKernelGGL(pack_kernel<float>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, m->W32[l], Rlo,
                                m->P[l], m->P[l]);
         e = hipGetLastError();
+        if (e == hipSuccess && (st = repack_direct(m.get(), l, 0))) { cleanup(); return st; }
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) { cleanup(); return from_hip(e, "weight packing"); }
         (void)hipFree(tmp);
@@ -1561,6 +1638,10 @@ int pcd_pc_model_destroy(pcd_model* m) {
         (void)hipFree(m->WT[l]);
         (void)hipFree(m->bias[l]);
         if (m->W32[l]) (void)hipFree(m->W32[l]);
+        if (!m->Wpk.empty()) {
+            (void)hipFree(m->Wpk[l]);
+            (void)hipFree(m->WTpk[l]);
+        }
     }
     delete m;
     return PCD_SUCCESS;
@@ -1610,6 +1691,14 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
         m->persist_grid = value;
     }
     else if (n == "ragged_order") m->ragged_order = value ? 1 : 0;
+    else if (n == "direct") {
+        if (value < 0 || value > 2) return fail(PCD_INVALID_VALUE, "direct must be 0, 1 or 2");
+        if (value == 2 && m->dtype == PCD_F32)
+            return fail(PCD_INVALID_VALUE, "direct = 2: the direct-weight tile takes 16-bit operands");
+        if (value == 2 && m->Wpk.empty())
+            if (int st = alloc_direct(m)) return st;
+        m->direct = value;
+    }
     else if (n == "k_stagger") {
         if (value < kKStaggerAuto || value > kMaxKStagger)
             return fail(PCD_INVALID_VALUE, "k_stagger must be -1 (automatic), 0 (off) or up to %d", kMaxKStagger);
@@ -2018,7 +2107,8 @@ static int refresh_operands(pcd_model* m, int l, hipStream_t s) {
                            m->P[l - 1], m->P[l - 1]);
         break;
     }
-    return from_hip(hipGetLastError(), "operand refresh");
+    if (int st = from_hip(hipGetLastError(), "operand refresh")) return st;
+    return repack_direct(m, l, s);
 }
 
 int pcd_pc_relax_clamped(pcd_model* m, const float* x0, const float* top, int batch, int steps, float* out_states,
@@ -2252,6 +2342,7 @@ static int learn_step(pcd_model* m, const float* x0, const float* labels, const 
             default: hipLaunchKernelGGL(hebbian_small_kernel<f16_t>, dim3(blocks), dim3(256), 0, s, hs); break;
             }
             st = from_hip(hipGetLastError(), "hebbian_small_kernel launch");
+            for (int l = l0; l < std::min(L, l0 + kHebbLayers) && !st; ++l) st = repack_direct(m, l, s);
         }
         if (energy_buf) {
             int st2 = pool_free(energy_buf, s);
@@ -2454,6 +2545,7 @@ static hipError_t upload_record_weights(pcd_model* m, int layer, const LayerReco
             hipLaunchKernelGGL(pack_record_kernel<float>, dim3(g1), dim3(256), 0, 0, codes, r.kind, scales, zeros, lo,
                                sz, 0, m->W32[layer], Rlo, m->P[layer]);
         e = hipGetLastError();
+        if (e == hipSuccess && repack_direct(m, layer, 0) != PCD_SUCCESS) e = hipErrorLaunchFailure;
         if (e == hipSuccess) e = hipDeviceSynchronize();
     }
     (void)hipFree(tmp);

@@ -11,9 +11,9 @@
 
 namespace pcd {
 
-// Launches phase_kernel<OP, BM, BN, epi> over `grid` workgroups of
-// TileCfg<BM, BN>::NT threads on `stream` and returns the launch status.
-template <typename OP, int BM, int BN>
+// Launches phase_kernel<OP, BM, BN, epi, WD> over `grid` workgroups of
+// TileCfg<BM, BN, *, WD>::NT threads on `stream` and returns the launch status.
+template <typename OP, int BM, int BN, bool WD = false>
 hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& args, int grid, hipStream_t stream);
 
 // Launches persistent_relax_kernel<OP, BM, BN> cooperatively over `grid`
@@ -24,9 +24,9 @@ extern template hipError_t launch_persistent_tile<float, 64, 64>(const PersistAr
 // Workgroups of persistent_relax_kernel<float, 64, 64> one CU holds at once.
 int persistent_blocks_per_cu();
 
-#define PCD_DECLARE_TILE(OP, BM, BN)                                                                    \
-    extern template hipError_t launch_phase_tile<OP, BM, BN>(int, const ProblemSet&, const PhaseArgs&, int, \
-                                                             hipStream_t);
+#define PCD_DECLARE_TILE(OP, BM, BN)                                                                           \
+    extern template hipError_t launch_phase_tile<OP, BM, BN, false>(int, const ProblemSet&, const PhaseArgs&, int, \
+                                                                    hipStream_t);
 #define PCD_DECLARE_OP(OP)         \
     PCD_DECLARE_TILE(OP, 32, 32)   \
     PCD_DECLARE_TILE(OP, 64, 64)   \
@@ -36,6 +36,10 @@ int persistent_blocks_per_cu();
 PCD_DECLARE_OP(float)
 PCD_DECLARE_OP(bf16_t)
 PCD_DECLARE_OP(f16_t)
+extern template hipError_t launch_phase_tile<bf16_t, 64, 128, true>(int, const ProblemSet&, const PhaseArgs&, int,
+                                                                    hipStream_t);
+extern template hipError_t launch_phase_tile<f16_t, 64, 128, true>(int, const ProblemSet&, const PhaseArgs&, int,
+                                                                   hipStream_t);
 #undef PCD_DECLARE_OP
 #undef PCD_DECLARE_TILE
 
