@@ -338,8 +338,13 @@ def traffic_from_pmc(workload, fetch_dir, write_dir, calib_fetch_dir, calib_writ
            "calibration": {"bytes": COPY_CALIB_BYTES, "fetch_kib": cf, "write_kib": cw,
                            "fetch_factor": f_fetch, "write_factor": f_write},
            "kernels": {}}
-    for name, tag in (("error_phase", ", 0>"), ("update_phase", ", 1>"), ("plain", ", 3>")):
-        sel = lambda n, tag=tag: "phase_kernel" in n and n.rstrip().endswith(tag + "(pcd::ProblemSet, pcd::PhaseArgs)")
+    import re
+    # phase_kernel<OP, BM, BN, EPI> or phase_kernel<OP, BM, BN, EPI, direct-weight flag>
+    epi_of = re.compile(r"phase_kernel<[^,<>]+, \d+, \d+, (\d)(?:, (?:true|false))?>\(pcd::ProblemSet, pcd::PhaseArgs\)")
+    for name, epi in (("error_phase", "0"), ("update_phase", "1"), ("plain", "3")):
+        def sel(n, epi=epi):
+            m = epi_of.search(n)
+            return m is not None and m.group(1) == epi
         fk, nf = _mean_counter(fr, "FETCH_SIZE", sel)
         wk, nw = _mean_counter(wr, "WRITE_SIZE", sel)
         if fk is None or wk is None:

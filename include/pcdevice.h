@@ -381,6 +381,14 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *                that still hold a running row, and deal only those tiles over
  *                the XCDs (default); 0: launch every tile, and let tiles whose
  *                rows have all finished return at once.  Results are the same.
+ *   direct       1: 16-bit batches of at most 64 rows take the direct-weight
+ *                tile (weights from a fragment-major copy straight into
+ *                registers) where the model keeps that copy, which 16-bit
+ *                models with at least one such tile per CU in their error
+ *                phase do (default); 0: the 64 x 64 tile; 2: the direct tile
+ *                for every 16-bit batch of at most 64 rows (the copy, as much
+ *                device memory as W and W^T, is made on first use).  A row's
+ *                bits depend on the tile.
  *   ragged_order 1: pcd_pc_relax_ragged settles the requests in decreasing
  *                step budget (rows permuted on the device and back), so rows
  *                that stop early fill whole row tiles that drop out (default);
