@@ -155,6 +155,7 @@ struct PhaseArgs {
     int k_stagger;              // > 1: K sweeps of tile (tm, tn) start (tm + tn) % k_stagger stages in
     const int* act_tm;          // ragged: row tiles with a row still running, increasing (nullable)
     const int* act_count;       // ragged: their number
+    int nt_store;               // settling epilogues store their full rows non-temporally
 };
 
 // How a phase's tiles are dealt over the XCDs.
@@ -480,7 +481,7 @@ __device__ __forceinline__ void stage_group(char* st, int g, f32x4 v, Pack pack)
 }
 template <int BYTES>
 __device__ __forceinline__ void flush_block(const char* st, void* out, size_t ld, int row0, int col0, uint64_t rmask,
-                                            int n, bool full) {
+                                            int n, bool full, bool nt = false) {
     const int lane = threadIdx.x & 63;
     if constexpr (BYTES == 4) {
         static_for<0, 4>([&](auto Pc) PCD_INLINE {
@@ -489,7 +490,8 @@ __device__ __forceinline__ void flush_block(const char* st, void* out, size_t ld
             float* dst = (float*)out + (size_t)(row0 + rr) * ld + col0 + cc;
             const bool rv = (rmask >> rr) & 1;
             if (full || (rv && col0 + cc + 3 < n)) {
-                gst4(dst, w);
+                if (nt) __builtin_nontemporal_store(w, (f32x4*)dst);
+                else gst4(dst, w);
             } else if (rv) {
                 static_for<0, 4>([&](auto K) PCD_INLINE {
                     constexpr int k = decltype(K)::value;
@@ -504,7 +506,8 @@ __device__ __forceinline__ void flush_block(const char* st, void* out, size_t ld
             uint16_t* dst = (uint16_t*)out + (size_t)(row0 + rr) * ld + col0 + cc;
             const bool rv = (rmask >> rr) & 1;
             if (full || (rv && col0 + cc + 7 < n)) {
-                *(__attribute__((address_space(1))) u32x4*)dst = w;
+                if (nt) __builtin_nontemporal_store(w, (u32x4*)dst);
+                else *(__attribute__((address_space(1))) u32x4*)dst = w;
             } else if (rv) {
                 static_for<0, 8>([&](auto K) PCD_INLINE {
                     constexpr int k = decltype(K)::value;
@@ -1247,6 +1250,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     auto trow = [&](int i) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + lr; };
     auto tcol = [&](int j, int g) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + 8 * g + 4 * half; };
     char* wstage = smem + 2 * wave_u * kStageWaveBytes;   // X / M_l values
+    const bool ntst = args.nt_store != 0;
     char* wstage2 = wstage + kStageWaveBytes;             // D / operand-copy values
     if constexpr (TR) __syncthreads();   // every wave is done reading the stage ring
     if constexpr (EPI == EPI_ERROR) {
@@ -1325,8 +1329,8 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
                     stage_group<OPB>(wstage2, g, dv, PackOp<OP>{});
                 });
                 const int brow = row0 + wm * C::WTM + i * 32, bcol = col0 + wn * C::WTN + j * 32;
-                if (P.eout && writer) flush_block<4>(wstage, P.eout, ldo, brow, bcol, rmask, P.N, full);
-                if (writer) flush_block<OPB>(wstage2, P.dout, ldo, brow, bcol, rmask, P.N, full);
+                if (P.eout && writer) flush_block<4>(wstage, P.eout, ldo, brow, bcol, rmask, P.N, full, ntst);
+                if (writer) flush_block<OPB>(wstage2, P.dout, ldo, brow, bcol, rmask, P.N, full, ntst);
                 if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
                 if constexpr (j == C::FN - 1) {
                     if (want_energy) {
@@ -1398,8 +1402,8 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
                 if (P.mop) stage_group<OPB>(wstage2, g, mn, PackOp<OP>{});
             });
             const int brow = row0 + wm * C::WTM + i * 32, bcol = col0 + wn * C::WTN + j * 32;
-            if (writer) flush_block<4>(wstage, P.m, ldo, brow, bcol, rmask, P.N, full);
-            if (P.mop && writer) flush_block<OPB>(wstage2, P.mop, ldo, brow, bcol, rmask, P.N, full);
+            if (writer) flush_block<4>(wstage, P.m, ldo, brow, bcol, rmask, P.N, full, ntst);
+            if (P.mop && writer) flush_block<OPB>(wstage2, P.mop, ldo, brow, bcol, rmask, P.N, full, ntst);
             if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
             __builtin_amdgcn_sched_barrier(0);
         });
