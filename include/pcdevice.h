@@ -392,6 +392,7 @@ int pcd_pc_model_info(const pcd_model* model, int* levels, int* sizes, int max_s
  *   nt_store     -1: the settling epilogues' row stores are non-temporal for
  *                16-bit models (default); 0: ordinary stores; 1: non-temporal.
  *                Results are the same.
+ *   nt_load      the same for the epilogues' loads of the fp32 states.
  *   ragged_order 1: pcd_pc_relax_ragged settles the requests in decreasing
  *                step budget (rows permuted on the device and back), so rows
  *                that stop early fill whole row tiles that drop out (default);

@@ -156,6 +156,7 @@ struct PhaseArgs {
     const int* act_tm;          // ragged: row tiles with a row still running, increasing (nullable)
     const int* act_count;       // ragged: their number
     int nt_store;               // settling epilogues store their full rows non-temporally
+    int nt_load;                // settling epilogues load their fp32 state rows non-temporally
 };
 
 // How a phase's tiles are dealt over the XCDs.
@@ -524,12 +525,14 @@ __device__ __forceinline__ void flush_block(const char* st, void* out, size_t ld
 // l % 32).  Read transposed directly, every four lanes would ask for four
 // rows, four times the requests of whole rows.
 __device__ __forceinline__ void load_block_rows(f32x4 (&raw)[4], const float* src, size_t ld, int row0, int col0,
-                                                int m, int n) {
+                                                int m, int n, bool nt = false) {
     const int lane = threadIdx.x & 63;
     static_for<0, 4>([&](auto Pc) PCD_INLINE {
         constexpr int p = decltype(Pc)::value;
         const int rr = (lane >> 3) + 8 * p, cc = (lane & 7) * 4;
-        raw[p] = (row0 + rr < m && col0 + cc < n) ? gld4(src + (size_t)(row0 + rr) * ld + col0 + cc) : f32x4{};
+        const float* a = src + (size_t)(row0 + rr) * ld + col0 + cc;
+        raw[p] = (row0 + rr < m && col0 + cc < n) ? (nt ? __builtin_nontemporal_load((const f32x4*)a) : gld4(a))
+                                                  : f32x4{};
     });
 }
 __device__ __forceinline__ void transpose_block(char* st, const f32x4 (&raw)[4], f32x4 (&tr)[4]) {
@@ -1250,7 +1253,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     auto trow = [&](int i) PCD_INLINE { return row0 + wm * C::WTM + i * 32 + lr; };
     auto tcol = [&](int j, int g) PCD_INLINE { return col0 + wn * C::WTN + j * 32 + 8 * g + 4 * half; };
     char* wstage = smem + 2 * wave_u * kStageWaveBytes;   // X / M_l values
-    const bool ntst = args.nt_store != 0;
+    const bool ntst = args.nt_store != 0, ntld = args.nt_load != 0;
     char* wstage2 = wstage + kStageWaveBytes;             // D / operand-copy values
     if constexpr (TR) __syncthreads();   // every wave is done reading the stage ring
     if constexpr (EPI == EPI_ERROR) {
@@ -1278,7 +1281,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             auto load_block = [&](auto Bc) PCD_INLINE {
                 constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
                 load_block_rows(mraw[b % PD], P.mlow, ldo, row0 + wm * C::WTM + i * 32, col0 + wn * C::WTN + j * 32,
-                                P.M, P.N);
+                                P.M, P.N, ntld);
             };
             static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
             float esum = 0.f;
@@ -1369,7 +1372,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         auto load_block = [&](auto Bc) PCD_INLINE {
             constexpr int b = decltype(Bc)::value, i = b / C::FN, j = b % C::FN;
             load_block_rows(xraw[b % PD], src, ldo, row0 + wm * C::WTM + i * 32, col0 + wn * C::WTN + j * 32, P.M,
-                            P.N);
+                            P.N, ntld);
         };
         static_for<0, PD>([&](auto Bc) PCD_INLINE { load_block(Bc); });
         uint64_t rmask = 0;

@@ -376,6 +376,7 @@ struct pcd_model {
     int ragged_order = 1;               // ragged requests settle in decreasing step budget (0: caller's order)
     int direct = 1;                     // direct-weight tile: 0 never, 1 where direct_eligible, 2 every batch <= 64 rows
     int nt_store = -1;                  // settling epilogues' stores non-temporal: -1 automatic (see relax_args), 0, 1
+    int nt_load = -1;                   // settling epilogues' fp32 state loads non-temporal: -1 automatic, 0, 1
     float prof_err_ms = 0.f, prof_upd_ms = 0.f;
     int prof_launches = 0;
     uint64_t clock = 0;
@@ -804,12 +805,13 @@ PhaseArgs relax_args(const pcd_model* m, const Workspace* w, const RelaxSpec& r,
     }
     args.row_req = r.row_req;
     args.done_at = r.done_at;
-    // Non-temporal epilogue stores for 16-bit models (same box, two runs each:
-    // c5 +2.1%, c5s +5.4%, c3 +0.3%); fp32 models keep ordinary stores (c2
-    // -1.4% with them: its 4 MB states are read again from the caches; c1 and
-    // c4 unchanged).
-    if (m->nt_store >= 0) args.nt_store = m->nt_store;
-    else args.nt_store = m->dtype != PCD_F32;
+    // Non-temporal epilogue stores and fp32 state loads for 16-bit models
+    // (same box, two runs each; stores: c5 +2.1%, c5s +5.4%, c3 +0.3%; loads on
+    // top: c5 +1.4%, c3 +0.35%, c5s unchanged).  fp32 models keep ordinary
+    // ones (c2 -1.4% with the stores, -1% with the loads: its 4 MB states are
+    // read again from the caches by the next phase; c1 and c4 unchanged).
+    args.nt_store = m->nt_store >= 0 ? m->nt_store : m->dtype != PCD_F32;
+    args.nt_load = m->nt_load >= 0 ? m->nt_load : m->dtype != PCD_F32;
     const bool need_energy = r.energy_out != nullptr || r.row_req != nullptr;
     if (!need_energy) args.energy_part = nullptr;
     return args;
@@ -1699,9 +1701,9 @@ int pcd_pc_set_option(pcd_model* m, const char* name, int value) {
         m->persist_grid = value;
     }
     else if (n == "ragged_order") m->ragged_order = value ? 1 : 0;
-    else if (n == "nt_store") {
-        if (value < -1 || value > 1) return fail(PCD_INVALID_VALUE, "nt_store must be -1 (automatic), 0 or 1");
-        m->nt_store = value;
+    else if (n == "nt_store" || n == "nt_load") {
+        if (value < -1 || value > 1) return fail(PCD_INVALID_VALUE, "%s must be -1 (automatic), 0 or 1", name);
+        (n == "nt_store" ? m->nt_store : m->nt_load) = value;
     }
     else if (n == "direct") {
         if (value < 0 || value > 2) return fail(PCD_INVALID_VALUE, "direct must be 0, 1 or 2");
