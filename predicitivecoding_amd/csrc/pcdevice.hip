@@ -311,7 +311,7 @@ struct Workspace {
     std::vector<float*> E;             // [L] X_l = M_l - eta (E_l + lambda sign M_l), 1 <= l <= L-2, fp32 [cap x P_l]
     float* energy_part = nullptr;      // [slots x cap]
     int slots_cap = 0;
-    float* split_part = nullptr;       // split-K partial tiles, kSplitPartTiles x 128 x 128 fp32
+    float* split_part = nullptr;       // split-K partial tiles, split_part_tiles() x 128 x 128 fp32
     int* split_count = nullptr;        // split-K finished-range counters, zero between launches
     int* act_tm = nullptr;             // ragged: row tiles still running at the current step [cap / kMinTileM]
     int* act_count = nullptr;          // ragged: their number
@@ -521,11 +521,15 @@ int max_energy_slots(const pcd_model* m) {
 // tiles as CUs, tiles of at most 128 x 128) cuts each tile's K into up to
 // cus / tiles (<= kMaxSplit) ranges of at least kSplitMinStages stages; the partial tiles
 // go to workspace scratch and the range that finishes last reduces them and
-// runs the epilogue.  Units of a phase never exceed the CU count, so the
-// scratch holds `cus` partial tiles of 128 x 128 and as many counters.
+// runs the epilogue.  The scratch holds `cus` partial tiles of 128 x 128, or
+// 4 and 16 times as many of 64 x 64 and 32 x 32, and a counter per split tile
+// (at most half the partial tiles: a split tile has two ranges or more);
+// assign_split decides how much of it a phase may use.
 int split_part_tiles(const pcd_model* m) { return std::max(m->cus, 1); }
+constexpr int kSplitCountsPerPart = 8;   // counters per 128 x 128 of scratch: the 32 x 32 tile's 16 / 2
 // Bytes of the split-K counters, whole 16-byte units so a zero kernel covers them.
-size_t split_count_bytes(const pcd_model* m) { return round_up((size_t)split_part_tiles(m) * 4, 16); }
+size_t split_count_bytes(int part_tiles) { return round_up((size_t)part_tiles * kSplitCountsPerPart * 4, 16); }
+size_t split_count_bytes(const pcd_model* m) { return split_count_bytes(split_part_tiles(m)); }
 
 
 int split_factor(int cus, int split_k, long tiles, Tile tile) {
@@ -550,8 +554,9 @@ int stage_k(int dtype, Tile tile) {
 }
 
 // The split-K plan of a phase or a GEMM: every problem's split factor and its
-// share of the partial-tile scratch (`part`, room for `budget` tiles of up to
-// 128 x 128) and of the counters (`count`, as many).
+// share of the partial-tile scratch (`part`, room for `budget` partial tiles of
+// 128 x 128, that is budget * 128 * 128 / (BM * BN) of a BM x BN tile) and of
+// the counters (`count`, budget * kSplitCountsPerPart of them).
 struct SplitScratch {
     float* part = nullptr;
     int* count = nullptr;
@@ -581,13 +586,24 @@ void assign_split(int cus, int split_k, int dtype, Tile tile, const SplitScratch
     // All or nothing: a phase whose splits do not all fit the scratch splits
     // none of its problems (splitting only the first ones would leave those
     // slower than the rest: c5s's phases, 11 problems of 16 tiles per XCD).
-    long need = 0;
+    long need = 0, need_counters = 0;
     for (auto& ps : sets)
         for (int i = 0; i < ps.n; ++i) {
             const int ks = wanted(ps.p[i]);
-            if (ks > 1) need += (long)ps.p[i].tiles_m * ps.p[i].tiles_n * ks;
+            if (ks > 1) {
+                need += (long)ps.p[i].tiles_m * ps.p[i].tiles_n * ks;
+                need_counters += (long)ps.p[i].tiles_m * ps.p[i].tiles_n;
+            }
         }
-    const bool fits = need <= sc.budget;
+    // A few-tiles phase (f > 1: half the CUs or more idle unsplit) gets the
+    // scratch counted in partial tiles of its own size: the 32 x 32 tile's
+    // phases need many (3072-512-128-10's update splits 32 tiles eight ways
+    // and 8 tiles four ways, 288 partial tiles of 32 x 32).  Balance splits of
+    // phases with more tiles keep the budget of `sc.budget` partial tiles of
+    // any size: given more, they made 2048 x 6 bf16 at 128 rows (64 x 64
+    // tiles, each CU holding its share at once) 78% slower.
+    const long budget = f > 1 ? sc.budget * (128L * 128) / ((long)tile.m * tile.n) : sc.budget;
+    const bool fits = need <= budget && need_counters <= sc.budget * kSplitCountsPerPart;
     long units = 0, counters = 0;
     for (auto& ps : sets)
         for (int i = 0; i < ps.n; ++i) {
@@ -1397,7 +1413,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     void* part = nullptr;
     if (!st && tile.m * tile.n <= 128 * 128 && p.tiles * 2 <= cus) {
         sc.budget = cus;
-        const size_t part_bytes = (size_t)sc.budget * 128 * 128 * 4, cnt_bytes = round_up((size_t)sc.budget * 4, 16);
+        const size_t part_bytes = (size_t)sc.budget * 128 * 128 * 4, cnt_bytes = split_count_bytes((int)sc.budget);
         if (!(st = pool_alloc(&part, part_bytes + cnt_bytes, s))) {
             sc.part = (float*)part;
             sc.count = (int*)((char*)part + part_bytes);
