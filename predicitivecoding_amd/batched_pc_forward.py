@@ -14,6 +14,7 @@ I/O for benchmarks, and ragged request batches with early exit.
 from __future__ import annotations
 
 import ctypes
+import threading
 import weakref
 
 import numpy as np
@@ -38,6 +39,70 @@ def _check_ragged_tables(offs: np.ndarray, steps: np.ndarray) -> None:
         raise ArgumentOutOfRangeException("steps")
 
 
+def _free_stage(ptrs: list) -> None:
+    """Returns a staging set's buffers to the library's pools (pinned host
+    pair first, then the device pair)."""
+    if ptrs:
+        h_in, h_out, d_in, d_out = ptrs
+        _native.lib().pcd_host_free(ctypes.c_void_p(h_in))
+        _native.lib().pcd_host_free(ctypes.c_void_p(h_out))
+        _native.lib().pcd_free_async(ctypes.c_void_p(d_in), None)
+        _native.lib().pcd_free_async(ctypes.c_void_p(d_out), None)
+        ptrs.clear()
+
+
+class _TopStage:
+    """Pinned host and device buffers a model keeps for its top-only host
+    settlings (the drop-in's calls): the input rows are written straight into
+    pinned memory, and the input copy, the settling and the top copy queue on
+    one stream behind one synchronisation, with nothing allocated per call.
+    Grown to the largest batch seen; one caller at a time (`lock`)."""
+
+    def __init__(self, s0: int, s_top: int):
+        self.s0, self.s_top = s0, s_top
+        self.rows = 0
+        self.ptrs: list = []
+        self.lock = threading.Lock()
+        self._finalizer = weakref.finalize(self, _free_stage, self.ptrs)
+
+    def ensure(self, rows: int) -> None:
+        if rows <= self.rows:
+            return
+        cap = max(rows, 2 * self.rows)
+        _free_stage(self.ptrs)
+        self.rows = 0
+        got = []
+        try:
+            for nbytes, fn in ((cap * self.s0 * 4, "pcd_host_alloc"), (cap * self.s_top * 4, "pcd_host_alloc")):
+                p = ctypes.c_void_p()
+                call(fn, ctypes.byref(p), nbytes)
+                got.append(p.value)
+            for nbytes in (cap * self.s0 * 4, cap * self.s_top * 4):
+                p = ctypes.c_void_p()
+                call("pcd_malloc_async", ctypes.byref(p), nbytes, None)
+                got.append(p.value)
+            call("pcd_device_synchronize")   # the pool's blocks are ready for any stream
+        except BaseException:
+            for i, q in enumerate(got):
+                if i < 2:
+                    _native.lib().pcd_host_free(ctypes.c_void_p(q))
+                else:
+                    _native.lib().pcd_free_async(ctypes.c_void_p(q), None)
+            raise
+        self.ptrs.extend(got)
+        self.rows = cap
+
+    def view(self, which: int, rows: int, cols: int) -> np.ndarray:
+        """[rows x cols] float32 array over pinned buffer `which` (0 input, 1 top)."""
+        buf = (ctypes.c_float * (rows * cols)).from_address(self.ptrs[which])
+        return np.frombuffer(buf, dtype=np.float32).reshape(rows, cols)
+
+    def close(self) -> None:
+        with self.lock:
+            self._finalizer()
+            self.rows = 0
+
+
 class PcDeviceModel:
     """A GenerativeSnapshot uploaded to the current GPU in one operand dtype."""
 
@@ -59,8 +124,10 @@ class PcDeviceModel:
              wp, bp, prec, DTYPE[dtype], ctypes.byref(h))
         self.handle = h.value
         self._finalizer = weakref.finalize(self, _native.lib().pcd_pc_model_destroy, self.handle)
+        self._stage = _TopStage(self.sizes[0], self.sizes[-1])
 
     def close(self) -> None:
+        self._stage.close()
         self._finalizer()
         self.handle = None
 
@@ -94,6 +161,10 @@ class PcDeviceModel:
             raise ArgumentException("Empty batch.")
         if steps < 1:
             raise ArgumentOutOfRangeException("inferenceSteps")
+        if not want_states and not want_energy:
+            top = self._relax_top_staged(B, steps, lambda v: np.copyto(v, x0), stream)
+            if top is not None:
+                return top, None, None
         dx = DeviceTensor.from_host(x0)
         top = DeviceTensor((B, self.sizes[-1]))
         st = DeviceTensor((B * sum(self.sizes),)) if want_states else None
@@ -117,6 +188,27 @@ class PcDeviceModel:
                 if t is not None:
                     t.free()
         return top_h, states, energy
+
+    def _relax_top_staged(self, B: int, steps: int, fill, stream: Stream | None = None):
+        """Top-only settling through the model's staging buffers: `fill` writes
+        the [B x s_0] input rows into pinned memory; returns the [B x s_top]
+        top as a new array, or None when another caller holds the staging set
+        (that caller's call then takes the allocating path)."""
+        st = self._stage
+        if not st.lock.acquire(blocking=False):
+            return None
+        try:
+            st.ensure(B)
+            h_in, h_out, d_in, d_out = st.ptrs
+            fill(st.view(0, B, self.sizes[0]))
+            sh = stream.handle if stream else None
+            call("pcd_memcpy_async", d_in, h_in, B * self.sizes[0] * 4, MEMCPY["h2d"], sh)
+            self.relax_device(d_in, B, steps, d_out, stream=stream)
+            call("pcd_memcpy_async", h_out, d_out, B * self.sizes[-1] * 4, MEMCPY["d2h"], sh)
+            call("pcd_stream_synchronize", sh)
+            return st.view(1, B, self.sizes[-1]).copy()
+        finally:
+            st.lock.release()
 
     def relax_ragged_device(self, x0_ptr: int, row_offsets, steps, top_ptr: int, exit_rule: str = "none",
                             exit_threshold: float = 0.0, stream: Stream | None = None):
@@ -351,6 +443,7 @@ class PcDeviceModel:
              int(bool(ffg)), None, None, (ctypes.c_float * L)(*precisions), DTYPE[dtype], ctypes.byref(h))
         self.handle = h.value
         self._finalizer = weakref.finalize(self, _native.lib().pcd_pc_model_destroy, self.handle)
+        self._stage = _TopStage(self.sizes[0], self.sizes[-1])
         for l, r in enumerate(records):
             self.load_record(l, r)
         return self
@@ -427,5 +520,8 @@ class BatchedPcForward:
         if dtype is None:
             dtype = "f16" if mixed else "f32"
         dev = BatchedPcForward._model(model, dtype)
-        top, _, _ = dev.relax(np.stack(rows), inference_steps)
-        return [top[i].copy() for i in range(top.shape[0])]
+        # rows stacked straight into the model's pinned input buffer
+        top = dev._relax_top_staged(len(rows), inference_steps, lambda v: np.stack(rows, out=v))
+        if top is None:
+            top, _, _ = dev.relax(np.stack(rows), inference_steps)
+        return list(top)

@@ -143,3 +143,73 @@ def test_drop_in_sees_the_snapshot_as_made(oracle):
     ref2, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, W, b, P, x, 8)
     assert max_rel(new, ref2) < 1e-4
     assert not np.allclose(new, first)
+
+
+def _allocating_top(model, x, steps):
+    """The top through per-call device buffers and synchronous copies."""
+    from predicitivecoding_amd import DeviceTensor
+    from predicitivecoding_amd.device import DeviceRuntime
+    dx = DeviceTensor.from_host(x)
+    top = DeviceTensor((x.shape[0], model.sizes[-1]))
+    try:
+        model.relax_device(dx.ptr, x.shape[0], steps, top.ptr)
+        DeviceRuntime.synchronize()
+        return top.to_host()
+    finally:
+        dx.free()
+        top.free()
+
+
+def test_staged_top_path_matches_allocating_path(oracle):
+    # Top-only host settlings go through the model's pinned staging buffers,
+    # grown to the largest batch seen.  Batches that grow and shrink give the
+    # same bits as per-call device buffers, and the oracle's values.
+    from predicitivecoding_amd import BatchedPcForward, PcDeviceModel
+    snap, W, b, P = _trained_snapshot(oracle, seed=41)
+    m = PcDeviceModel(snap, "f32")
+    try:
+        for B in (5, 33, 12, 70, 1, 70):
+            x = make_inputs(B, 6, seed=100 + B, dist="uniform11")
+            staged, _, _ = m.relax(x, 8)
+            assert np.array_equal(staged, _allocating_top(m, x, 8)), B
+            ref, _, _ = oracle.batched_relax(SIZES, "tanh", 0.1, W, b, P, x, 8)
+            assert max_rel(staged, ref) < 1e-4, B
+            rows = BatchedPcForward.infer_get_top_batch(snap, list(x), 8)
+            assert len(rows) == B and all(np.array_equal(r, staged[i]) for i, r in enumerate(rows))
+    finally:
+        m.close()
+
+
+def test_staged_top_path_under_concurrent_callers(oracle):
+    # Two threads settle on one model at once: one holds the staging set, the
+    # other takes the allocating path; both get the single-caller bits.
+    import threading
+
+    from predicitivecoding_amd import PcDeviceModel, Stream
+    snap, _, _, _ = _trained_snapshot(oracle, seed=42)
+    m = PcDeviceModel(snap, "f32")
+    xs = [make_inputs(40, 6, seed=200 + t, dist="uniform11") for t in range(2)]
+    want = [m.relax(x, 9)[0] for x in xs]
+    got, errors = [[None] * 6 for _ in range(2)], []
+
+    def worker(t):
+        s = Stream()
+        try:
+            for i in range(6):
+                got[t][i] = m.relax(xs[t], 9, stream=s)[0]
+        except Exception as e:   # reported below
+            errors.append(e)
+        finally:
+            s.close()
+
+    try:
+        threads = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join(timeout=60)
+        assert not errors, errors
+        for t in range(2):
+            assert all(np.array_equal(g, want[t]) for g in got[t])
+    finally:
+        m.close()

@@ -677,6 +677,26 @@ def test_split_k_small_batches(oracle, sizes, batch, act):
     assert np.array_equal(a[0], e[0]) and np.array_equal(a[2], e[2])
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_published_network_split_k(oracle, dtype):
+    # The reference's published workload (tools/MixedPrecisionBench/Program.cs:75-127):
+    # [3072, 512, 128, 10] tanh, eta 0.05, 64 samples, 20 steps.  Its update
+    # phase has 42 tiles of 32 x 32: layer 1 (K = 3072) splits eight ways and
+    # layer 2 (K = 512) four, 288 partial tiles of 32 x 32 in the scratch.
+    snap, W, b, P, x = build_case([3072, 512, 128, 10], "tanh", 0.05, batch=64, seed=23)
+    a = run_gpu(snap, x, 20, dtype, states=True, energy=True)
+    n = run_gpu(snap, x, 20, dtype, states=True, energy=True, options={"split_k": 0})
+    r = run_oracle(oracle, snap, W, b, P, x, 20, dtype, states=True, energy=True)
+    tol = 1e-4 if dtype == "f32" else 2e-3
+    for name, got in (("split", a), ("unsplit", n)):
+        errs = dict(top=max_rel(got[0], r[0]), energy=max_rel(got[2], r[2]),
+                    states=max(max_rel(g, q) for g, q in zip(got[1], r[1])))
+        _report(f"published network {dtype} {name}", **errs)
+        assert all(v < tol for v in errs.values()), errs
+    # the split sums K in another order: some state's bits differ from the unsplit run
+    assert any(not np.array_equal(g, h) for g, h in zip(a[1], n[1]))
+
+
 def test_split_k_repeated_graph_replays():
     # the same plan replayed many times in a row keeps giving the same answer
     snap, _, _, _, x = build_case([500, 700, 9], "tanh", 0.1, batch=12, seed=22)
