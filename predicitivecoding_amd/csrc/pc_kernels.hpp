@@ -1436,6 +1436,11 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     } else {  // EPI_PLAIN: C = alpha acc + beta C
         if (!writer) return;   // no barrier follows
         const float alpha = args.alpha, beta = args.beta;
+        // whole tiles of an output too large to stay in the caches store non-temporally
+        auto put = [&](float* p, float v) PCD_INLINE {
+            if (ntst) __builtin_nontemporal_store(v, p);
+            else gst(p, v);
+        };
         static_for<0, C::FM>([&](auto I) PCD_INLINE {
             constexpr int i = decltype(I)::value;
             static_for<0, C::FN>([&](auto J) PCD_INLINE {
@@ -1450,12 +1455,12 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
                         });
                         static_for<0, 16>([&](auto R) PCD_INLINE {
                             constexpr int r = decltype(R)::value;
-                            gst(P.m + base_of(i, j) + rstep(r), alpha * acc[i][j][r] + beta * cv[r]);
+                            put(P.m + base_of(i, j) + rstep(r), alpha * acc[i][j][r] + beta * cv[r]);
                         });
                     } else {
                         static_for<0, 16>([&](auto R) PCD_INLINE {
                             constexpr int r = decltype(R)::value;
-                            gst(P.m + base_of(i, j) + rstep(r), alpha * acc[i][j][r]);
+                            put(P.m + base_of(i, j) + rstep(r), alpha * acc[i][j][r]);
                         });
                     }
                 } else {

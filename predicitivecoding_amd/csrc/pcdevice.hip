@@ -1340,6 +1340,10 @@ int pcd_event_elapsed_ms(float* ms, void* start, void* end) {
 // product: a tile wider than the product (rounded up to 64) in either
 // dimension would be mostly padding, in MFMA work and in packed operand
 // memory, however many products there are.
+// Provider outputs of at least this many bytes (twice the chip's L2) are
+// stored non-temporally: a caller reads them long after the L2 has turned over.
+constexpr size_t kGemmNtBytes = (size_t)64 << 20;
+
 static Tile choose_gemm_tile(int dtype, int m, int n, int cus, int batch = 1) {
     auto tiles = [&](int t) { return (long)batch * ((m + t - 1) / t) * ((n + t - 1) / t); };
     auto fits = [&](int t) { return t <= (int)round_up(m, 64) && t <= (int)round_up(n, 64); };
@@ -1426,6 +1430,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     a.alpha = 1.f;
     a.beta = beta;
     a.k_stagger = dtype == PCD_F32 ? 0 : auto_k_stagger(kp / stage_k(dtype, tile));
+    a.nt_store = (size_t)m * n * 4 >= kGemmNtBytes;
     if (!st) st = launch_phase(dtype, tile, EPI_PLAIN, sets[0], a, s);
     release();
     if (part) {
@@ -1474,6 +1479,7 @@ static int gemm_batched_common(int dtype, const void* dA, const void* dB, float*
     a.alpha = 1.f;
     a.beta = 0.f;
     a.k_stagger = dtype == PCD_F32 ? 0 : auto_k_stagger(kp / stage_k(dtype, tile));
+    a.nt_store = (size_t)batch * m * n * 4 >= kGemmNtBytes;
     for (int i0 = 0; i0 < batch && !st; i0 += kMaxProblems) {
         ProblemSet ps;
         std::memset(&ps, 0, sizeof ps);
