@@ -38,14 +38,24 @@ def make_inputs(batch, size, seed=1, dist="normal"):
     raise ValueError(dist)
 
 
-def close(a, b, tol):
-    """The reference tests' element bound |a-b| <= tol*(1+|b|) (BatchedPcForwardTests.cs:67)."""
+def _rel(a, b):
+    """Elementwise |a-b| / (1+|b|), with equal values (infinities of one sign,
+    NaN against NaN) at 0 and a NaN or an infinity on one side only at inf, so
+    a diverging network compares by where it overflowed and no NaN reaches a
+    reduction (Python's max() skips a NaN that is not its first argument)."""
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)
-    return bool(np.all(np.abs(a - b) <= tol * (1.0 + np.abs(b))))
+    same = (a == b) | (np.isnan(a) & np.isnan(b))
+    with np.errstate(invalid="ignore"):
+        d = np.abs(a - b) / (1.0 + np.abs(b))
+    return np.where(same, 0.0, np.where(np.isnan(d), np.inf, d))
+
+
+def close(a, b, tol):
+    """The reference tests' element bound |a-b| <= tol*(1+|b|) (BatchedPcForwardTests.cs:67)."""
+    return bool(np.all(_rel(a, b) <= tol))
 
 
 def max_rel(a, b):
-    a = np.asarray(a, dtype=np.float64)
-    b = np.asarray(b, dtype=np.float64)
-    return float(np.max(np.abs(a - b) / (1.0 + np.abs(b)))) if a.size else 0.0
+    d = _rel(a, b)
+    return float(np.max(d)) if d.size else 0.0
