@@ -332,6 +332,9 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
 #ifndef PCD_ERR_PD
 #define PCD_ERR_PD 3   // error epilogue: blocks whose M operands are in flight
 #endif
+#ifndef PCD_EPI_BATCH
+#define PCD_EPI_BATCH 1   // epilogue operand loads in batches of PD blocks (0: one block at a time)
+#endif
 #ifndef PCD_BIG_RB
 #define PCD_BIG_RB 128
 #endif
@@ -480,6 +483,23 @@ __device__ __forceinline__ void stage_group(char* st, int g, f32x4 v, Pack pack)
     if constexpr (BYTES == 4) *(f32x4*)(st + lr * kStageRowBytes + (8 * g + 4 * half) * 4) = v;
     else *(u32x2*)(st + lr * kStageRowBytes + (8 * g + 4 * half) * 2) = pack(v);
 }
+// The epilogues' operand loads after block B of NB, PD blocks in flight.
+// Loads and stores share vmcnt and may complete out of order with each other,
+// so once a block's stores are out, a wait for an older load is a wait for
+// every vector-memory operation (the compiler emits vmcnt(0)).  A load issued
+// after every block would put the next block's wait behind it: a full memory
+// round trip per 32 x 32 block.  The next PD blocks' loads therefore go out
+// together after the last block of a batch, and only the batch's first block
+// waits (one round trip per PD blocks, its loads all in flight at once).
+template <int B, int PD, int NB, typename F> __device__ __forceinline__ void next_operands(F&& load_block) {
+#if PCD_EPI_BATCH
+    if constexpr ((B + 1) % PD == 0 && B + 1 < NB)
+        static_for<B + 1, (B + 1 + PD < NB ? B + 1 + PD : NB)>([&](auto Bc) PCD_INLINE { load_block(Bc); });
+#else
+    if constexpr (B + PD < NB) load_block(std::integral_constant<int, B + PD>{});
+#endif
+}
+
 template <int BYTES>
 __device__ __forceinline__ void flush_block(const char* st, void* out, size_t ld, int row0, int col0, uint64_t rmask,
                                             int n, bool full, bool nt = false) {
@@ -1264,9 +1284,8 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         // compiles several times faster.
         auto epilogue = [&](auto ActC) PCD_INLINE {
             constexpr int ACT = decltype(ActC)::value;
-            // Blocks b = i*FN + j in order; the M_{l-1} operands of the next PD
-            // blocks are in flight while a block computes, so the load latency is
-            // paid about once per tile instead of once per block.
+            // Blocks b = i*FN + j in order, their M_{l-1} operands loaded PD
+            // blocks at a time (next_operands).
             constexpr int NB = C::FM * C::FN, PD = NB < PCD_ERR_PD ? NB : PCD_ERR_PD;
             const float P_low = P.prec, inv2p = 0.5f / P.prec;
             const float eta = args.eta, lam = args.act_reg;
@@ -1334,7 +1353,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
                 const int brow = row0 + wm * C::WTM + i * 32, bcol = col0 + wn * C::WTN + j * 32;
                 if (P.eout && writer) flush_block<4>(wstage, P.eout, ldo, brow, bcol, rmask, P.N, full, ntst);
                 if (writer) flush_block<OPB>(wstage2, P.dout, ldo, brow, bcol, rmask, P.N, full, ntst);
-                if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
+                next_operands<b, PD, NB>(load_block);
                 if constexpr (j == C::FN - 1) {
                     if (want_energy) {
                         // The two half-waves hold the two column halves of each group.
@@ -1363,7 +1382,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         // M_l = X_l + eta G for the layers below the top, X_l = M_l - eta (E_l +
         // lambda sign M_l) having been written by the error phase; the top
         // layer (E = 0) reads M_l itself: M_l -= eta (lambda sign M_l - G).
-        // The operand of the next PD blocks is in flight while a block computes.
+        // The operands are loaded PD blocks at a time (next_operands).
         constexpr int NB = C::FM * C::FN, PD = NB < 3 ? NB : 3;
         const float eta = args.eta, lam = args.act_reg;
         const bool folded = P.eself != nullptr;
@@ -1407,7 +1426,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             const int brow = row0 + wm * C::WTM + i * 32, bcol = col0 + wn * C::WTN + j * 32;
             if (writer) flush_block<4>(wstage, P.m, ldo, brow, bcol, rmask, P.N, full, ntst);
             if (P.mop && writer) flush_block<OPB>(wstage2, P.mop, ldo, brow, bcol, rmask, P.N, full, ntst);
-            if constexpr (b + PD < NB) load_block(std::integral_constant<int, b + PD>{});
+            next_operands<b, PD, NB>(load_block);
             __builtin_amdgcn_sched_barrier(0);
         });
     } else if constexpr (EPI == EPI_FFG) {
