@@ -1327,27 +1327,41 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
                         const float pre = acc[i][j][4 * g + k] + bv[k];
                         float y, dy;
                         act_eval(ACT >= 0 ? ACT : args.act, pre, y, dy);
-                        const float m = mv[g][k];
-                        const float e = P_low * (m - y);
+                        const float e = P_low * (mv[g][k] - y);
                         dv[k] = dy * e;
-                        // The state's own part of its update, folded here while
-                        // M_{l-1} is in registers: X = M - eta (e + lambda sign M).
-                        // The update phase then only adds eta * (W^T D).
-                        float gr = e;
-                        if (lam > 0.f) gr += lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
-                        xv[k] = m - eta * gr;
                         ev[k] = e;
                     });
-                    float es = 0.f;
-                    if (rok && col + 3 < P.N) {
-                        es = ev[0] * ev[0] + ev[1] * ev[1] + ev[2] * ev[2] + ev[3] * ev[3];
-                    } else if (rok) {
+                    // The state's own part of its update, folded here while
+                    // M_{l-1} is in registers: X = M - eta (e + lambda sign M).
+                    // The update phase then only adds eta * (W^T D).  lambda = 0
+                    // (no activity regularisation) takes a branch of its own, with
+                    // the same bits (e + 0 is e): as one expression the sign's
+                    // compares and selects ran for every element whatever lambda.
+                    if (lam > 0.f) {
                         static_for<0, 4>([&](auto K) PCD_INLINE {
                             constexpr int k = decltype(K)::value;
-                            if (col + k < P.N) es += ev[k] * ev[k];
+                            const float m = mv[g][k];
+                            const float gr = ev[k] + lam * (m > 0.f ? 1.f : (m < 0.f ? -1.f : 0.f));
+                            xv[k] = m - eta * gr;
+                        });
+                    } else {
+                        static_for<0, 4>([&](auto K) PCD_INLINE {
+                            constexpr int k = decltype(K)::value;
+                            xv[k] = mv[g][k] - eta * ev[k];
                         });
                     }
-                    esum += es * inv2p;
+                    if (want_energy) {   // the row energies only when a caller reads them
+                        float es = 0.f;
+                        if (rok && col + 3 < P.N) {
+                            es = ev[0] * ev[0] + ev[1] * ev[1] + ev[2] * ev[2] + ev[3] * ev[3];
+                        } else if (rok) {
+                            static_for<0, 4>([&](auto K) PCD_INLINE {
+                                constexpr int k = decltype(K)::value;
+                                if (col + k < P.N) es += ev[k] * ev[k];
+                            });
+                        }
+                        esum += es * inv2p;
+                    }
                     stage_group<4>(wstage, g, xv, PackOp<OP>{});
                     stage_group<OPB>(wstage2, g, dv, PackOp<OP>{});
                 });
