@@ -32,31 +32,81 @@ __global__ void zero_segs_kernel(const ZeroSegs z) {
     }
 }
 
-// Pack a row-major [rows x cols] fp32 matrix (optionally read transposed) into
-// a zero-padded [prow x pcol] buffer of the operand type whose rows are `ldd`
-// elements apart (ldd >= pcol; the columns past pcol are left alone).
+// Pack a row-major [rows x cols] matrix (optionally read transposed: the
+// physical source is then [cols x rows]) into a zero-padded [prow x pcol]
+// buffer of the operand type whose rows are `ldd` elements apart (ldd >= pcol;
+// the columns past pcol are left alone).  An fp32 source is rounded to the
+// operand type; a 16-bit source of the operand's own type is copied bit for
+// bit.  A workgroup moves 64 x 64 tiles through LDS, so the source reads and
+// the destination writes are both row-contiguous whichever way the source is
+// read (one element per thread straight across a transpose reads one element
+// per 2-byte segment of a row).
 template <typename OP>
-__global__ void pack_kernel(const void* __restrict__ src, int src_is_f32, int rows, int cols, int trans,
-                            void* __restrict__ dst, int prow, int pcol, int ldd) {
-    size_t n = (size_t)prow * pcol;
-    for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < n; k += (size_t)gridDim.x * blockDim.x) {
-        int r = (int)(k / pcol), c = (int)(k % pcol);
-        const size_t i = (size_t)r * ldd + c;
-        float v = 0.f;
-        bool inside = r < rows && c < cols;
-        if (inside) {
-            // logical element (r, c) of op(src); physical src is [rows x cols] or [cols x rows]
-            size_t s = trans ? (size_t)c * rows + r : (size_t)r * cols + c;
-            if (src_is_f32) {
-                v = ((const float*)src)[s];
-            } else {
-                // 16-bit source of the operand's own type: copy the bits
-                ((uint16_t*)dst)[i] = ((const uint16_t*)src)[s];
-                continue;
+__global__ void __launch_bounds__(256) pack_kernel(const void* __restrict__ src, int src_is_f32, int rows, int cols,
+                                                   int trans, void* __restrict__ dst, int prow, int pcol, int ldd) {
+    __shared__ uint32_t tile[64][65];   // raw bits: fp32 values or 16-bit codes; 65 words a row, conflict-free
+    // Thread t moves 4 consecutive elements of a row: row t/16 (+16, +32, +48), elements 4 (t%16) .. +3.
+    const int q4 = (threadIdx.x & 15) * 4, qr = threadIdx.x >> 4;
+    const int c0 = blockIdx.x * 64, tiles_y = (prow + 63) / 64;
+    // the physical source: [rows x cols], or [cols x rows] read transposed
+    const int srows = trans ? cols : rows, scols = trans ? rows : cols;
+    // 4-element groups are 8- or 16-byte aligned where the row length and the base pointer allow it
+    const bool vec_src = (scols & 3) == 0 && ((uintptr_t)src & (src_is_f32 ? 15 : 7)) == 0;
+    const bool vec_dst = (ldd & 3) == 0 && ((uintptr_t)dst & (OpTraits<OP>::bytes * 4 - 1)) == 0;
+    for (int by = blockIdx.y; by < tiles_y; by += gridDim.y) {
+        const int r0 = by * 64;
+        const int sr0 = trans ? c0 : r0, sc0 = trans ? r0 : c0;   // the tile's origin in the physical source
+#pragma unroll
+        for (int i = qr; i < 64; i += 16) {
+            const int sr = sr0 + i, sc = sc0 + q4;
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+            if (sr < srows) {
+                const size_t at = (size_t)sr * scols + sc;
+                if (vec_src && sc + 3 < scols) {
+                    if (src_is_f32) {
+                        const u32x4 v = *(const u32x4*)((const float*)src + at);
+                        w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+                    } else {
+                        const u32x2 v = *(const u32x2*)((const uint16_t*)src + at);
+                        w[0] = v[0] & 0xFFFFu; w[1] = v[0] >> 16; w[2] = v[1] & 0xFFFFu; w[3] = v[1] >> 16;
+                    }
+                } else {
+                    for (int k = 0; k < 4; ++k)
+                        if (sc + k < scols)
+                            w[k] = src_is_f32 ? __float_as_uint(((const float*)src)[at + k]) : ((const uint16_t*)src)[at + k];
+                }
+            }
+            // physical (i, q4 + k) is logical (i, q4 + k), or (q4 + k, i) read transposed
+            for (int k = 0; k < 4; ++k) {
+                if (trans) tile[q4 + k][i] = w[k];
+                else tile[i][q4 + k] = w[k];
             }
         }
-        if (!inside && !src_is_f32) { ((uint16_t*)dst)[i] = 0; continue; }
-        OpTraits<OP>::store(dst, i, v);
+        __syncthreads();
+#pragma unroll
+        for (int i = qr; i < 64; i += 16) {
+            const int r = r0 + i, c = c0 + q4;
+            if (r >= prow || c >= pcol) continue;
+            const size_t at = (size_t)r * ldd + c;
+            uint32_t w[4];
+            for (int k = 0; k < 4; ++k) w[k] = tile[i][q4 + k];
+            if (vec_dst && c + 3 < pcol) {
+                if (src_is_f32) {
+                    const f32x4 v = {__uint_as_float(w[0]), __uint_as_float(w[1]), __uint_as_float(w[2]),
+                                     __uint_as_float(w[3])};
+                    if constexpr (OpTraits<OP>::bytes == 4) *(f32x4*)((float*)dst + at) = v;
+                    else *(u32x2*)((uint16_t*)dst + at) = OpTraits<OP>::pack4(v);
+                } else {
+                    *(u32x2*)((uint16_t*)dst + at) = u32x2{w[0] | (w[1] << 16), w[2] | (w[3] << 16)};
+                }
+            } else {
+                for (int k = 0; k < 4 && c + k < pcol; ++k) {
+                    if (src_is_f32) OpTraits<OP>::store(dst, at + k, __uint_as_float(w[k]));
+                    else ((uint16_t*)dst)[at + k] = (uint16_t)w[k];
+                }
+            }
+        }
+        __syncthreads();   // the next tile row reuses `tile`
     }
 }
 

@@ -517,6 +517,19 @@ int max_energy_slots(const pcd_model* m) {
     return slots;
 }
 
+// Launches pack_kernel over the [prow x pcol] destination: 64 x 64 tiles, a
+// column of tiles per workgroup column, about 4096 workgroups in all (each
+// walks down several tile rows when the matrix is large).
+template <typename OP>
+void pack_op(hipStream_t s, const void* src, int src_is_f32, int rows, int cols, int trans, void* dst, int prow,
+             int pcol, int ldd) {
+    const int tiles_x = (pcol + 63) / 64, tiles_y = (prow + 63) / 64;
+    const int gy = std::max(1, std::min({tiles_y, 65535, (4096 + tiles_x - 1) / tiles_x}));
+    const dim3 grid((unsigned)tiles_x, (unsigned)gy);
+    hipLaunchKernelGGL(pack_kernel<OP>, grid, dim3(256), 0, s, src, src_is_f32, rows, cols, trans, dst, prow, pcol,
+                       ldd);
+}
+
 // Split-K.  A phase whose output tiles leave CUs idle (at most half as many
 // tiles as CUs, tiles of at most 128 x 128) cuts each tile's K into up to
 // cus / tiles (<= kMaxSplit) ranges of at least kSplitMinStages stages; the partial tiles
@@ -1378,11 +1391,10 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     };
     const int src_f32 = dtype == PCD_F32;
     auto pack = [&](const void* src, int rows, int cols, int trans, void* dst, int prow, int pcol) -> int {
-        int grid = (int)std::min<size_t>(((size_t)prow * pcol + 255) / 256, 8192);
         switch (dtype) {
-        case PCD_F32: hipLaunchKernelGGL(pack_kernel<float>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
-        case PCD_BF16: hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
-        default: hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid), dim3(256), 0, s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
+        case PCD_F32: pack_op<float>(s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
+        case PCD_BF16: pack_op<bf16_t>(s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
+        default: pack_op<f16_t>(s, src, src_f32, rows, cols, trans, dst, prow, pcol, pcol); break;
         }
         return from_hip(hipGetLastError(), "pack_kernel launch");
     };
@@ -1631,24 +1643,22 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
         if (e == hipSuccess) e = hipMemcpy(bb, b[l - 1], (size_t)lo * 4, hipMemcpyHostToDevice);
         if (e != hipSuccess) { cleanup(); return from_hip(e, "hipMemcpy(weights)"); }
         // W_l as stored ([lo x sz] -> [Rlo x P_l]) and transposed ([sz x lo] -> [Rsz x P_{l-1}]).
-        int grid1 = (int)std::min<size_t>(((size_t)Rlo * m->P[l] + 255) / 256, 8192);
-        int grid2 = (int)std::min<size_t>(((size_t)Rsz * m->P[l - 1] + 255) / 256, 8192);
         switch (dtype) {
         case PCD_F32:
-            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
-            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
+            pack_op<float>(0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
+            pack_op<float>(0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
             break;
         case PCD_BF16:
-            hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
-            hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
+            pack_op<bf16_t>(0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
+            pack_op<bf16_t>(0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
             break;
         default:
-            hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
-            hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(grid2), dim3(256), 0, 0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
+            pack_op<f16_t>(0, tmp, 1, lo, sz, 0, w, Rlo, m->P[l], m->P[l]);
+            pack_op<f16_t>(0, tmp, 1, sz, lo, 1, wt, Rsz, m->P[l - 1], m->P[l - 1]);
             break;
         }
         if (m->W32[l])
-            hipLaunchKernelGGL(pack_kernel<float>, dim3(grid1), dim3(256), 0, 0, tmp, 1, lo, sz, 0, m->W32[l], Rlo,
+            pack_op<float>(0, tmp, 1, lo, sz, 0, m->W32[l], Rlo,
                                m->P[l], m->P[l]);
         e = hipGetLastError();
         if (e == hipSuccess && (st = repack_direct(m.get(), l, 0))) { cleanup(); return st; }
@@ -2123,23 +2133,21 @@ static int refresh_operands(pcd_model* m, int l, hipStream_t s) {
     const int lo = m->s[l - 1], sz = m->s[l];
     const int Rlo = (int)round_up(lo, kRowPad), Rsz = (int)round_up(sz, kRowPad);
     const void* src = m->dtype == PCD_F32 ? (const void*)m->W[l] : (const void*)m->W32[l];
-    const int g1 = (int)std::min<size_t>(((size_t)Rlo * m->P[l] + 255) / 256, 8192);
-    const int g2 = (int)std::min<size_t>(((size_t)Rsz * m->P[l - 1] + 255) / 256, 8192);
     switch (m->dtype) {
     case PCD_F32:
-        hipLaunchKernelGGL(pack_kernel<float>, dim3(g2), dim3(256), 0, s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
+        pack_op<float>(s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
                            m->P[l - 1], m->P[l - 1]);
         break;
     case PCD_BF16:
-        hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(g1), dim3(256), 0, s, src, 1, Rlo, m->P[l], 0, m->W[l], Rlo,
+        pack_op<bf16_t>(s, src, 1, Rlo, m->P[l], 0, m->W[l], Rlo,
                            m->P[l], m->P[l]);
-        hipLaunchKernelGGL(pack_kernel<bf16_t>, dim3(g2), dim3(256), 0, s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
+        pack_op<bf16_t>(s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
                            m->P[l - 1], m->P[l - 1]);
         break;
     default:
-        hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(g1), dim3(256), 0, s, src, 1, Rlo, m->P[l], 0, m->W[l], Rlo,
+        pack_op<f16_t>(s, src, 1, Rlo, m->P[l], 0, m->W[l], Rlo,
                            m->P[l], m->P[l]);
-        hipLaunchKernelGGL(pack_kernel<f16_t>, dim3(g2), dim3(256), 0, s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
+        pack_op<f16_t>(s, src, 1, m->P[l], lo, 1, m->WT[l], Rsz,
                            m->P[l - 1], m->P[l - 1]);
         break;
     }
@@ -2401,13 +2409,12 @@ static int learn_step(pcd_model* m, const float* x0, const float* labels, const 
         if ((st = pool_alloc(&mt, (size_t)Rsz * kp * 4, s))) break;
         tmp.push_back(mt);
         const int g1 = (int)std::min<size_t>(((size_t)Rlo * kp + 255) / 256, 8192);
-        const int g2 = (int)std::min<size_t>(((size_t)Rsz * kp + 255) / 256, 8192);
         const int gb = std::min((lo + 255) / 256, 1024);
         // D_l^T (D is in the operand type: a 16-bit model's update uses the
         // rounded Delta its settling's W^T GEMM consumed), M_l^T, and the bias
         switch (m->dtype) {
         case PCD_F32:
-            hipLaunchKernelGGL(pack_kernel<float>, dim3(g1), dim3(256), 0, s, (const void*)w->D[l], 1, m->P[l - 1],
+            pack_op<float>(s, (const void*)w->D[l], 1, m->P[l - 1],
                                batch, 1, dt, Rlo, kp, kp);
             hipLaunchKernelGGL(bias_update_kernel<float>, dim3(gb), dim3(256), 0, s, (const void*)w->D[l],
                                m->P[l - 1], batch, lo, m->bias[l], eta_w);
@@ -2425,7 +2432,7 @@ static int learn_step(pcd_model* m, const float* x0, const float* labels, const 
                                m->P[l - 1], batch, lo, m->bias[l], eta_w);
             break;
         }
-        hipLaunchKernelGGL(pack_kernel<float>, dim3(g2), dim3(256), 0, s, (const void*)w->M[l], 1, m->P[l], batch, 1,
+        pack_op<float>(s, (const void*)w->M[l], 1, m->P[l], batch, 1,
                            mt, Rsz, kp, kp);
         if ((st = from_hip(hipGetLastError(), "learning-step packing"))) break;
         if (sets.empty() || sets.back().n == kMaxProblems) {

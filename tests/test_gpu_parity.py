@@ -752,3 +752,44 @@ def test_gemm_provider_shapes(dtype, m, k, n, ta, tb):
     err = np.max(np.abs(got - want)) / (1 + np.max(np.abs(want)))
     print(f"gemm {dtype} {m}x{k}x{n} ta={ta} tb={tb} err={err:.2e}", flush=True)
     assert err < 1e-5
+
+
+@pytest.mark.parametrize("dtype,m,k,n,ta,tb", [
+    ("f32", 200, 516, 130, 0, 0),     # row lengths a multiple of 4: the vector pack paths
+    ("f32", 131, 257, 67, 1, 0),      # ragged rows: per-element packing
+    ("bf16", 256, 512, 384, 0, 0),
+    ("bf16", 99, 130, 250, 1, 1),
+])
+def test_gemm_provider_packs_unaligned_operands(dtype, m, k, n, ta, tb):
+    # Operands one element past an aligned address (a caller's sub-array): the
+    # operand packing must not assume 8- or 16-byte aligned rows.  Against
+    # float64 of the same operand values.
+    from predicitivecoding_amd import DeviceTensor
+    from predicitivecoding_amd._native import call
+    rng = np.random.default_rng(11)
+    A = rng.standard_normal((k, m) if ta else (m, k)).astype(np.float32)
+    B = rng.standard_normal((n, k) if tb else (k, n)).astype(np.float32)
+    if dtype == "bf16":
+        from oracle import pc_oracle
+        Ab, Bb = pc_oracle.bf16_bits(A), pc_oracle.bf16_bits(B)
+        A = (Ab.astype(np.uint32) << 16).view(np.float32)
+        B = (Bb.astype(np.uint32) << 16).view(np.float32)
+        hA, hB = Ab.ravel(), Bb.ravel()
+        esz, pad = 2, np.zeros(1, np.uint16)
+    else:
+        hA, hB = A.ravel(), B.ravel()
+        esz, pad = 4, np.zeros(1, np.float32)
+    # each operand stored one element into its buffer
+    dA = DeviceTensor.from_host(np.concatenate([pad, hA]))
+    dB = DeviceTensor.from_host(np.concatenate([pad, hB]))
+    dC = DeviceTensor.from_host(np.zeros((m, n), np.float32))
+    try:
+        call(f"pcd_gemm_{dtype}", dA.ptr + esz, dB.ptr + esz, dC.ptr, m, k, n, ta, tb, 0.0, None)
+        got = dC.to_host()
+    finally:
+        for t in (dA, dB, dC):
+            t.free()
+    want = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    err = np.max(np.abs(got - want)) / (1 + np.max(np.abs(want)))
+    print(f"gemm unaligned {dtype} {m}x{k}x{n} ta={ta} tb={tb} err={err:.2e}", flush=True)
+    assert err < 1e-5
