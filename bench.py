@@ -760,6 +760,56 @@ def bench_published(args, standalone=False):
     return rec
 
 
+def vendor_gemm_context(sizes, B, dtype, reps=5, ramp_s=0.15):
+    """The vendor library on the same box, in the same run: hipBLASLt (through
+    torch.mm) computing the plain products of one error phase -- for every
+    layer l, [B x s_l] @ [s_l x s_{l-1}] in `dtype`, each layer with its own
+    operands and output, no epilogue.  Context for the roofline fraction of
+    the fused phases (what a library GEMM of the same shapes reaches on this
+    power-limited part), never a number this build reports as its own.
+    Warm-up runs past the clock's ramp at process start (~50 ms) before the
+    timed passes; HIP events on torch's stream, on which the products run."""
+    import torch
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    L = len(sizes)
+    A = [torch.randn((B, sizes[l]), device="cuda", dtype=tdt, generator=gen) for l in range(1, L)]
+    Wt = [(torch.randn((sizes[l], sizes[l - 1]), device="cuda", dtype=torch.float32, generator=gen)
+           * sizes[l] ** -0.5).to(tdt) for l in range(1, L)]
+    out = [torch.empty((B, sizes[l - 1]), device="cuda", dtype=tdt) for l in range(1, L)]
+
+    def one_phase():
+        for a, w, o in zip(A, Wt, out):
+            torch.mm(a, w, out=o)
+
+    one_phase()   # the library's first calls choose and load their kernels
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 1
+    while n < 3 or time.perf_counter() - t0 < ramp_s:
+        one_phase()
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        one_phase()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    flop = 2.0 * B * sum(sizes[l] * sizes[l - 1] for l in range(1, L))
+    rec = {"library": f"hipBLASLt via torch.mm (torch {torch.__version__})", "ms_per_phase": ms,
+           "tflops": flop / (ms * 1e-3) / 1e12, "frac": flop / (ms * 1e-3) / PEAK[dtype],
+           "what": f"the plain {dtype} products of one error phase ({L - 1} layers, {dtype} out, no epilogue), "
+                   f"mean of {reps} passes after {n} warm-up passes"}
+    del A, Wt, out
+    torch.cuda.empty_cache()
+    return rec
+
+
 def bench_settle(args, name, cfg, steps, warmup, cpu_budget, pcie=False):
     """One fixed-batch settling workload (c1, c2, c3, c5, c5s): `steps` timed
     passes of pcd_pc_relax on inputs resident in HBM after `warmup` untimed
@@ -846,6 +896,11 @@ def bench_settle(args, name, cfg, steps, warmup, cpu_budget, pcie=False):
               f"{achieved / 1e12:.1f} TFLOP/s = {100 * achieved / peak:.1f}% of peak, "
               f"{bytes_launch / (dom_ms * 1e-3) / 1e9:.0f} GB/s algorithmic", file=sys.stderr, flush=True)
     roofline.update(traffic_fields(sizes, B, cfg["dtype"]))
+    if roofline["bound"] == "mfma" and cfg["dtype"] in ("bf16", "f16") and not args.no_vendor:
+        roofline["vendor_gemm"] = vendor_gemm_context(sizes, B, cfg["dtype"])
+        v = roofline["vendor_gemm"]
+        print(f"# vendor GEMM (same shapes, plain): {v['ms_per_phase']:.4f} ms per phase, "
+              f"{v['tflops']:.0f} TFLOP/s = {100 * v['frac']:.1f}% of peak", file=sys.stderr, flush=True)
 
     pcie_rec = None
     if pcie:
@@ -914,6 +969,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="default (c5) line only: leave out the c3 and published-workload records")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="leave out the same-shape hipBLASLt context of the 16-bit settling records")
     ap.add_argument("--cpu-budget", type=float, default=20.0,
                     help="seconds the CPU baseline sample is sized for (its calibration overestimates ~2x)")
     ap.add_argument("--tile", type=int, default=0, help="force the GEMM tile rows (and columns unless --tile-n)")
