@@ -142,7 +142,9 @@ int pcd_event_elapsed_ms(float* ms, void* start, void* end);
  * CudaGemmProvider.MatMulDeviceEx (Gemm/CudaGemmProvider.cs:82-98): op(A) is
  * A [m,k] or, with trans_a, the transpose of a physical [k,m] A (same for B).
  * With trans_a = trans_b = 0 and beta = 0 this is MatMulDevice (:62-72).
- * Scratch for operand packing comes from the library's pool. */
+ * Operands are read where they lie when aligned and whole-tile shaped
+ * (16-bit B also in its row-major [k,n] layout, transposed in LDS); others
+ * are packed into scratch from the library's pool. */
 int pcd_gemm_f32(const float* dA, const float* dB, float* dC, int m, int k, int n,
                  int trans_a, int trans_b, float beta, void* stream);
 /* bf16 operands (raw bf16 bit patterns), fp32 accumulation and fp32 C:

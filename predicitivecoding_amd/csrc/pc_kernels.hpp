@@ -55,6 +55,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Keeps
 // accumulator indices constant however large the body, where #pragma unroll
@@ -68,7 +69,12 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 enum Act { ACT_LINEAR = 0, ACT_TANH = 1, ACT_RELU = 2, ACT_SIGMOID = 3, ACT_GELU = 4 };
-enum Epi { EPI_ERROR = 0, EPI_UPDATE = 1, EPI_FFG = 2, EPI_PLAIN = 3 };
+// EPI_PLAIN_KN: the plain product with the B operand row-major [K x N] (the
+// layout of Gemm.MatMul's B), read where it lies: each stage's K rows of the
+// tile's columns go into LDS as they are and the MFMA fragments come out of
+// them through gfx950's transposing LDS read (ds_read_b64_tr_b16), so the
+// operand is never packed.  16-bit operands, LDS-operand tiles only.
+enum Epi { EPI_ERROR = 0, EPI_UPDATE = 1, EPI_FFG = 2, EPI_PLAIN = 3, EPI_PLAIN_KN = 4 };
 
 // Global-memory accessors.  The epilogue pointers arrive through the
 // kernel-argument struct as generic pointers; accessing them through the
@@ -97,7 +103,7 @@ struct f16_t { uint16_t v; };
 // One GEMM of a grouped launch plus the operands of its epilogue.
 struct Problem {
     const void* A;        // [>= tiles_m*BM rows x lda], K-contiguous
-    const void* B;        // [>= tiles_n*BN rows x ldb], K-contiguous
+    const void* B;        // [>= tiles_n*BN rows x ldb], K-contiguous (EPI_PLAIN_KN: [K rows x ldb], N-contiguous)
     int lda, ldb;         // leading dimensions, elements
     int M, N, K;          // valid rows, valid columns, K (a multiple of the stage depth)
     int tiles_m, tiles_n;  // tile grid of the output
@@ -323,6 +329,16 @@ __device__ __forceinline__ bool row_active(const PhaseArgs& a, int row) {
 // 2-way conflict.
 template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
     return unit ^ ((row / (256 / RB)) % (RB / 16));
+}
+// Row-major B stages (EPI_PLAIN_KN): 16-byte unit u of K row k sits at unit
+// u ^ kn_swz(k).  A transposing fragment read of 32 lanes covers four K rows
+// and the same 64 bytes of each; the XOR puts those four pieces on four
+// different 64-byte bank windows (LDS: 64 banks of 4 bytes).  Rows of 256 or
+// more bytes are a whole number of bank periods, so rows k % 4 = 0..3 take
+// windows 0..3 by the XOR alone; 128-byte rows (BN = 64) already alternate
+// halves, and the XOR separates k and k + 2.
+template <int BN> __device__ __forceinline__ int kn_swz(int k) {
+    return BN >= 128 ? (k & 3) * 4 : ((k >> 1) & 1) * 4;
 }
 
 // Build-time tile parameters (K bytes per row per stage: *_RB; LDS ring
@@ -915,9 +931,14 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // miss.  The sum over K is taken in that rotated order, so a row's result
     // depends on the row tile it falls in (still the same run to run).
     const int koff = (!C::WD && args.k_stagger > 1 && nk > 0) ? ((tm + tn) % args.k_stagger) % nk : 0;
-    const char* Ag = (const char*)P.A + (size_t)row0 * P.lda * OPB + (size_t)kb * C::RB;
-    const char* Bg = (const char*)P.B + (size_t)col0 * P.ldb * OPB + (size_t)kb * C::RB;
+    // B row-major [K x N] (EPI_PLAIN_KN): ldb is its row pitch, a stage is KE
+    // of its rows, and the tile's columns start col0 elements into each row.
+    constexpr bool BKN = EPI == EPI_PLAIN_KN;
+    static_assert(!BKN || (OPB == 2 && C::KW == 1 && !C::WD), "row-major B: 16-bit operands, LDS-operand tiles");
     const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
+    const char* Ag = (const char*)P.A + (size_t)row0 * lda_b + (size_t)kb * C::RB;
+    const char* Bg = BKN ? (const char*)P.B + (size_t)col0 * OPB + (size_t)kb * KE * ldb_b
+                         : (const char*)P.B + (size_t)col0 * ldb_b + (size_t)kb * C::RB;
 
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
@@ -1004,20 +1025,36 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // This lane's source of each of its wave's QPW loads per stage: combined
     // stage row R = q*ROWS_PER_LOAD + lane/UNITS (A rows, then B rows),
     // physical unit lane%UNITS, which holds logical unit swz(R, lane%UNITS).
+    // Row-major B (BKN) instead fills the stage's B region (KE rows of BN
+    // elements) as it lies in memory, row after row, each row's 16-byte units
+    // permuted by kn_swz so that the transposing fragment reads below are
+    // conflict-free: the lane that writes region byte ob copies row ob / (BN
+    // OPB), unit (ob % (BN OPB)) / 16 ^ kn_swz(row).  A stage then advances
+    // the B source by KE rows.
     const char* src[C::QPW];
 #pragma unroll
     for (int i = 0; i < C::QPW; ++i) {
         const int q = wave_u * C::QPW + i;
         const int R = q * C::ROWS_PER_LOAD + lane / C::UNITS;
         const int unit = swz<C::RB>(R, lane % C::UNITS);
-        src[i] = R < BM ? Ag + (size_t)R * lda_b + unit * 16 : Bg + (size_t)(R - BM) * ldb_b + unit * 16;
+        if (BKN && R >= BM) {
+            const int ob = (q * C::ROWS_PER_LOAD - BM) * C::RB + lane * 16;
+            const int kr = ob / (BN * OPB);
+            src[i] = Bg + (size_t)kr * ldb_b + ((ob % (BN * OPB)) / 16 ^ kn_swz<BN>(kr)) * 16;
+        } else {
+            src[i] = R < BM ? Ag + (size_t)R * lda_b + unit * 16 : Bg + (size_t)(R - BM) * ldb_b + unit * 16;
+        }
     }
+    const size_t bstep = BKN ? (size_t)KE * ldb_b : (size_t)C::RB;   // source bytes per stage of B loads
     auto issue_stage = [&](int kt) PCD_INLINE {
         const uint32_t base = lds0 + (kt % C::NS) * C::stage_bytes + wave_u * C::QPW * 1024;
         int kk = kt + koff;
         if (kk >= nk) kk -= nk;
 #pragma unroll
-        for (int i = 0; i < C::QPW; ++i) lds_dma16(src[i] + (size_t)kk * C::RB, base + i * 1024);
+        for (int i = 0; i < C::QPW; ++i) {
+            const bool bload = (wave_u * C::QPW + i) * 1024 >= BM * C::RB;   // wave-uniform
+            lds_dma16(src[i] + (size_t)kk * (bload ? bstep : (size_t)C::RB), base + i * 1024);
+        }
     };
     // Fragments of K chunk c (32 bytes per row) of the stage in `slot`.
     auto read_frags = [&](int slot, int c, u32x4* a, u32x4* b) PCD_INLINE {
@@ -1029,8 +1066,28 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         }
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) {
-            const int R = BM + wn * C::WTN + j * 32 + lr;
-            b[j] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
+            if constexpr (BKN) {
+                // Lane l takes column n0 + l % 32 and K rows 16c + 8 (l / 32) + 0..7
+                // of the stage, in two transposing reads of four rows each: in each
+                // group of 16 lanes, lane i reads row kbase + i / 4, columns
+                // 4 (i % 4) .. + 3 of the group's 16, and lane j receives element
+                // j % 4 of lanes j / 4, 4 + j / 4, 8 + j / 4 and 12 + j / 4, i.e.
+                // column j of rows kbase .. kbase + 3.
+                const char* bst = st + BM * C::RB;
+                const int n = wn * C::WTN + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+                u32x2 h[2];
+                static_for<0, 2>([&](auto Hc) PCD_INLINE {
+                    const int k = 16 * c + 8 * half + 4 * decltype(Hc)::value + ((lane & 15) >> 2);
+                    const char* p = bst + k * (BN * OPB) + ((n * OPB) ^ (kn_swz<BN>(k) * 16));
+                    h[decltype(Hc)::value] = __builtin_bit_cast(
+                        u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                   (__attribute__((address_space(3))) v4i16*)(__attribute__((address_space(3))) char*)p));
+                });
+                b[j] = u32x4{h[0][0], h[0][1], h[1][0], h[1][1]};
+            } else {
+                const int R = BM + wn * C::WTN + j * 32 + lr;
+                b[j] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
+            }
         }
     };
     auto mfmas = [&](const u32x4* a, const u32x4* b) PCD_INLINE {
@@ -1072,15 +1129,25 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // One LDS fragment read after each of the chunk's first MFMAs, the rest of
     // the MFMAs after them.
     constexpr int NMF = C::FM * C::FN * (F32OP ? 4 : 1);   // MFMAs per chunk
-    constexpr int NRD = C::FM + C::FN;                     // fragment reads per chunk
+    constexpr int NRD = C::FM + C::FN * (BKN ? 2 : 1);     // fragment reads per chunk
     auto interleave = [&]() PCD_INLINE {
         // MFMA first: the chunk's first MFMA then waits only on fragments read
         // before it, not on the read just issued (bf16 phases +1%).
-        static_for<0, NRD>([&](auto) PCD_INLINE {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        });
-        if constexpr (NMF > NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
+        if constexpr (BKN) {
+            constexpr int NP = NMF < NRD ? NMF : NRD;
+            static_for<0, NP>([&](auto) PCD_INLINE {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            });
+            if constexpr (NMF > NP) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NP, 0);
+            if constexpr (NRD > NP) __builtin_amdgcn_sched_group_barrier(0x100, NRD - NP, 0);
+        } else {
+            static_for<0, NRD>([&](auto) PCD_INLINE {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            });
+            if constexpr (NMF > NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
+        }
     };
     const int c0 = wk * C::NCW;   // this wave's first chunk of a stage
     for (int s2 = 0; s2 < C::D && s2 < nk; ++s2) issue_stage(s2);

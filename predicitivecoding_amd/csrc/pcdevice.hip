@@ -1383,11 +1383,15 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     auto aligned = [&](const void* p) { return ((uintptr_t)p % 16) == 0; };
     const bool direct_a = !trans_a && m == mp && k == kp && aligned(dA);
     const bool direct_b = trans_b && n == np && k == kp && aligned(dB);
+    // B in Gemm.MatMul's own row-major [k x n] layout, with whole tiles of
+    // columns and K a whole number of stages, is read where it lies too, on the
+    // 16-bit tiles that transpose it in LDS (EPI_PLAIN_KN).
+    const bool kn_b = !trans_b && kn_tile(ob, tile.m, tile.n, false) && n == np && k == kp && aligned(dB);
     void *pa = nullptr, *pb = nullptr;
     int st = PCD_SUCCESS;
     auto release = [&]() {
         if (pa && !direct_a) pool_free(pa, s);
-        if (pb && !direct_b) pool_free(pb, s);
+        if (pb && !direct_b && !kn_b) pool_free(pb, s);
     };
     const int src_f32 = dtype == PCD_F32;
     auto pack = [&](const void* src, int rows, int cols, int trans, void* dst, int prow, int pcol) -> int {
@@ -1404,7 +1408,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     if (direct_a) pa = (void*)dA;
     else if (!(st = pool_alloc(&pa, (size_t)mp * kp * ob, s))) st = pack(dA, m, k, trans_a, pa, mp, kp);
     if (!st) {
-        if (direct_b) pb = (void*)dB;
+        if (direct_b || kn_b) pb = (void*)dB;
         else if (!(st = pool_alloc(&pb, (size_t)np * kp * ob, s))) st = pack(dB, n, k, trans_b ? 0 : 1, pb, np, kp);
     }
     std::vector<ProblemSet> sets(1);
@@ -1414,7 +1418,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     p.A = pa;
     p.lda = kp;
     p.B = pb;
-    p.ldb = kp;
+    p.ldb = kn_b ? n : kp;   // the row pitch of row-major B, else of the K-contiguous copy
     p.M = m;
     p.N = n;
     p.K = kp;
@@ -1443,7 +1447,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     a.beta = beta;
     a.k_stagger = dtype == PCD_F32 ? 0 : auto_k_stagger(kp / stage_k(dtype, tile));
     a.nt_store = (size_t)m * n * 4 >= kGemmNtBytes;
-    if (!st) st = launch_phase(dtype, tile, EPI_PLAIN, sets[0], a, s);
+    if (!st) st = launch_phase(dtype, tile, kn_b ? EPI_PLAIN_KN : EPI_PLAIN, sets[0], a, s);
     release();
     if (part) {
         int st2 = pool_free(part, s);
@@ -1470,9 +1474,13 @@ static int gemm_batched_common(int dtype, const void* dA, const void* dB, float*
     const int mp = (int)round_up(m, tile.m), np = (int)round_up(n, tile.n), kp = (int)round_up(k, kFeatPad);
     const int ob = op_bytes(dtype);
     const size_t a_item = (size_t)mp * kp * ob, b_item = (size_t)np * kp * ob;
+    // Each B_i [k x n] is read where it lies (EPI_PLAIN_KN) when the tile has
+    // that form, its columns fill whole tiles, K is a whole number of stages and
+    // every item starts 16-byte aligned.
+    const bool kn_b = kn_tile(ob, tile.m, tile.n, false) && n == np && k == kp && (uintptr_t)dB % 16 == 0;
     void *pa = nullptr, *pb = nullptr;
     int st = pool_alloc(&pa, a_item * batch, s);
-    if (!st) st = pool_alloc(&pb, b_item * batch, s);
+    if (!st && !kn_b) st = pool_alloc(&pb, b_item * batch, s);
     auto pack = [&](const void* src, int rows, int cols, int trans, void* dst, int prow, int pcol) -> int {
         const int grid = (int)std::min<size_t>(((size_t)batch * prow * pcol + 255) / 256, 16384);
         const int f32 = dtype == PCD_F32;
@@ -1485,7 +1493,7 @@ static int gemm_batched_common(int dtype, const void* dA, const void* dB, float*
     };
     // the kernel's A is A_i [m x k]; its B is B_i^T [n x k] (B_i read transposed)
     if (!st) st = pack(dA, m, k, 0, pa, mp, kp);
-    if (!st) st = pack(dB, n, k, 1, pb, np, kp);
+    if (!st && !kn_b) st = pack(dB, n, k, 1, pb, np, kp);
     PhaseArgs a;
     std::memset(&a, 0, sizeof a);
     a.alpha = 1.f;
@@ -1501,8 +1509,8 @@ static int gemm_batched_common(int dtype, const void* dA, const void* dB, float*
             Problem& p = ps.p[q];
             p.A = (const char*)pa + i * a_item;
             p.lda = kp;
-            p.B = (const char*)pb + i * b_item;
-            p.ldb = kp;
+            p.B = kn_b ? (const void*)((const char*)dB + i * (size_t)k * n * ob) : (const void*)((const char*)pb + i * b_item);
+            p.ldb = kn_b ? n : kp;
             p.M = m;
             p.N = n;
             p.K = kp;
@@ -1512,7 +1520,7 @@ static int gemm_batched_common(int dtype, const void* dA, const void* dB, float*
             p.ldo = n;
             p.m = dC + i * (size_t)m * n;
         }
-        st = launch_phase(dtype, tile, EPI_PLAIN, ps, a, s);
+        st = launch_phase(dtype, tile, kn_b ? EPI_PLAIN_KN : EPI_PLAIN, ps, a, s);
     }
     if (pa) {
         int st2 = pool_free(pa, s);

@@ -31,6 +31,13 @@ hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& ar
     case EPI_ERROR: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_ERROR, WD>), dim3(grid), block, 0, s, set, args); break;
     case EPI_UPDATE: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_UPDATE, WD>), dim3(grid), block, 0, s, set, args); break;
     case EPI_FFG: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_FFG, WD>), dim3(grid), block, 0, s, set, args); break;
+    case EPI_PLAIN_KN:
+        if constexpr (kn_tile(OpTraits<OP>::bytes, BM, BN, WD)) {
+            hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN_KN, WD>), dim3(grid), block, 0, s, set, args);
+            break;
+        } else {
+            return hipErrorInvalidValue;   // no row-major-B form of this tile
+        }
     default: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN, WD>), dim3(grid), block, 0, s, set, args); break;
     }
     return hipGetLastError();

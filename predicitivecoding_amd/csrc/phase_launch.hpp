@@ -11,6 +11,12 @@
 
 namespace pcd {
 
+// Tiles with a row-major-B plain product (EPI_PLAIN_KN): 16-bit operands on
+// the LDS-operand tiles the GEMM provider uses.
+constexpr bool kn_tile(int op_bytes, int bm, int bn, bool wd) {
+    return op_bytes == 2 && !wd && bm == bn && (bm == 64 || bm == 128 || bm == 256);
+}
+
 // Launches phase_kernel<OP, BM, BN, epi, WD> over `grid` workgroups of
 // TileCfg<BM, BN, *, WD>::NT threads on `stream` and returns the launch status.
 template <typename OP, int BM, int BN, bool WD = false>

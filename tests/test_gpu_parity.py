@@ -715,8 +715,13 @@ def test_split_k_repeated_graph_replays():
     ("f32", 64, 4096, 64, 0, 0),        # one output tile, long K: split over 8 workgroups
     ("f32", 128, 2048, 192, 1, 1),      # transposed operands, split-K
     ("bf16", 1024, 1024, 1024, 0, 1),   # both operands read where they lie (no packing)
-    ("bf16", 4096, 4096, 4096, 0, 0),   # 256 x 256 tiles
+    ("bf16", 4096, 4096, 4096, 0, 0),   # 256 x 256 tiles, row-major B read in place
     ("f16", 300, 777, 1000, 1, 0),      # ragged shape, packed
+    # row-major B read where it lies and transposed in LDS, on each tile that does it
+    ("f16", 4096, 1024, 4096, 0, 0),    # 256 x 256
+    ("f16", 512, 256, 8192, 0, 0),      # 128 x 128
+    ("bf16", 64, 512, 2048, 0, 0),      # 64 x 64, split-K
+    ("bf16", 1024, 192, 1024, 1, 0),    # 64 x 64, A packed, three K stages
 ])
 def test_gemm_provider_shapes(dtype, m, k, n, ta, tb):
     # CudaGemmProvider.MatMulDeviceEx semantics (C = op(A) op(B) + beta C) on the
