@@ -896,7 +896,7 @@ def bench_settle(args, name, cfg, steps, warmup, cpu_budget, pcie=False):
               f"{achieved / 1e12:.1f} TFLOP/s = {100 * achieved / peak:.1f}% of peak, "
               f"{bytes_launch / (dom_ms * 1e-3) / 1e9:.0f} GB/s algorithmic", file=sys.stderr, flush=True)
     roofline.update(traffic_fields(sizes, B, cfg["dtype"]))
-    if roofline["bound"] == "mfma" and cfg["dtype"] in ("bf16", "f16") and not args.no_vendor:
+    if roofline["bound"] == "mfma" and cfg["dtype"] in ("bf16", "f16") and not (args.no_vendor or args.no_extra):
         roofline["vendor_gemm"] = vendor_gemm_context(sizes, B, cfg["dtype"])
         v = roofline["vendor_gemm"]
         print(f"# vendor GEMM (same shapes, plain): {v['ms_per_phase']:.4f} ms per phase, "
@@ -968,7 +968,9 @@ def main():
     ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="default (c5) line only: leave out the c3 and published-workload records")
+                    help="leave out the c3 and published-workload records of the default (c5) line and the "
+                         "same-shape hipBLASLt context (the profiling runs use it: their traces hold this library's "
+                         "kernels only)")
     ap.add_argument("--no-vendor", action="store_true",
                     help="leave out the same-shape hipBLASLt context of the 16-bit settling records")
     ap.add_argument("--cpu-budget", type=float, default=20.0,
