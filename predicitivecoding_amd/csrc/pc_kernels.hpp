@@ -83,6 +83,7 @@ enum Epi { EPI_ERROR = 0, EPI_UPDATE = 1, EPI_FFG = 2, EPI_PLAIN = 3, EPI_PLAIN_
 typedef __attribute__((address_space(1))) float gfloat;
 typedef __attribute__((address_space(1))) uint16_t gu16;
 typedef __attribute__((address_space(1))) int gint;
+typedef __attribute__((address_space(1))) unsigned long long gu64;
 __device__ __forceinline__ float gld(const float* p) { return *(const gfloat*)p; }
 __device__ __forceinline__ int gld(const int* p) { return *(const gint*)p; }
 __device__ __forceinline__ void gst(float* p, float v) { *(gfloat*)p = v; }
@@ -647,7 +648,7 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
         // each wave publishes its group's two 64-bit words per lane; the range
         // that finishes last sums every range's group in range order.
         typedef unsigned long long u64;
-        u64* part = (u64*)(P.part + (size_t)tile * ks * (BM * BN));
+        gu64* part = (gu64*)(P.part + (size_t)tile * ks * (BM * BN));   // global, not flat: see flush_block
         constexpr int UNIT = BM * BN / 2;
         const int slot = (wave * 64 + lane) * 2;
         auto pack = [](float a, float b) PCD_INLINE { return (u64)__float_as_uint(a) | ((u64)__float_as_uint(b) << 32); };
@@ -658,10 +659,10 @@ __device__ __forceinline__ void ksw_settle_tail(const Problem& P, const PhaseArg
         wait_vmcnt<0>();
         __syncthreads();
         int* flag = (int*)(ered + C::KW * 32);
-        if (tid == 0) *flag = __hip_atomic_fetch_add(P.count + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) *flag = __hip_atomic_fetch_add((gint*)(P.count + tile), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (*flag != ks - 1) return;
-        if (tid == 0) __hip_atomic_store(P.count + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+        if (tid == 0) __hip_atomic_store((gint*)(P.count + tile), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
         u64 pv[kMaxSplit][2];
         static_for<0, kMaxSplit>([&](auto Kc) PCD_INLINE {
             constexpr int k = decltype(Kc)::value;
@@ -891,7 +892,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     if (args.row_req != nullptr && n_act < 0) {
         // Any active row in the tile?  The flag borrows the first word of the
         // (not yet used) stage ring, which the full ring leaves no room beside.
-        volatile int* flag = (volatile int*)smem;
+        volatile __attribute__((address_space(3))) int* flag = (volatile __attribute__((address_space(3))) int*)smem;
         if (tid == 0) *flag = 0;
         __syncthreads();
         if (tid < BM) {
@@ -1256,10 +1257,10 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         // Lane-contiguous layout: block (i, j) of this wave holds each lane's 16
         // accumulators as 8 consecutive 64-bit pairs (a wave's block is 4 KB).
         typedef unsigned long long u64;
-        u64* part = (u64*)(P.part + (size_t)tile * ks * (BM * BN));
+        gu64* part = (gu64*)(P.part + (size_t)tile * ks * (BM * BN));   // global, not flat: see flush_block
         auto slot_of = [&](int i, int j) PCD_INLINE { return (((wmn * C::FM + i) * C::FN + j) * 64 + lane) * 8; };
         constexpr int UNIT = BM * BN / 2;   // 64-bit words of one partial tile
-        u64* mine = part + (size_t)split * UNIT;
+        gu64* mine = part + (size_t)split * UNIT;
         if (writer) {
             static_for<0, C::FM>([&](auto I) PCD_INLINE {
                 static_for<0, C::FN>([&](auto J) PCD_INLINE {
@@ -1277,11 +1278,11 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         __syncthreads();      // ... every lane's; the stage ring is no longer read
         int* flag = (int*)smem;
         if (tid == 0)
-            *flag = __hip_atomic_fetch_add(P.count + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = __hip_atomic_fetch_add((gint*)(P.count + tile), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         const bool last = *flag == ks - 1;
         if (!last) return;
-        if (tid == 0) __hip_atomic_store(P.count + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+        if (tid == 0) __hip_atomic_store((gint*)(P.count + tile), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
         // Per block, four ranges at a time: their words are all requested
         // before any is summed (two round trips for eight ranges), and the sum
         // runs over the ranges in order.
