@@ -798,3 +798,36 @@ def test_gemm_provider_packs_unaligned_operands(dtype, m, k, n, ta, tb):
     err = np.max(np.abs(got - want)) / (1 + np.max(np.abs(want)))
     print(f"gemm unaligned {dtype} {m}x{k}x{n} ta={ta} tb={tb} err={err:.2e}", flush=True)
     assert err < 1e-5
+
+
+@pytest.mark.parametrize("dtype,m,k,n", [
+    ("bf16", 4096, 1024, 4096),   # 256 x 256 tiles
+    ("f16", 512, 512, 8192),      # 128 x 128
+    ("bf16", 64, 1024, 2048),     # 64 x 64, split-K
+    ("f16", 1024, 192, 1024),     # 64 x 64, three K stages
+])
+def test_gemm_row_major_b_matches_transposed_b_bitwise(dtype, m, k, n):
+    # B in Gemm.MatMul's row-major [k x n] layout, transposed in LDS by the
+    # kernel, against the same B given transposed ([n x k], read as it lies):
+    # the MFMAs see the same operands in the same K order, so the products
+    # agree bit for bit.
+    import torch
+    from predicitivecoding_amd import DeviceTensor  # noqa: F401  (loads the library)
+    from predicitivecoding_amd._native import call
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m + k + n)
+    A = torch.randn((m, k), device="cuda", generator=g).to(tdt)
+    B = torch.randn((k, n), device="cuda", generator=g).to(tdt)
+    Bt = B.t().contiguous()
+    C1 = torch.empty((m, n), device="cuda", dtype=torch.float32)
+    C2 = torch.empty_like(C1)
+    call(f"pcd_gemm_{dtype}", A.data_ptr(), B.data_ptr(), C1.data_ptr(), m, k, n, 0, 0, 0.0, None)
+    call(f"pcd_gemm_{dtype}", A.data_ptr(), Bt.data_ptr(), C2.data_ptr(), m, k, n, 0, 1, 0.0, None)
+    torch.cuda.synchronize()
+    same = torch.equal(C1, C2)
+    print(f"gemm {dtype} {m}x{k}x{n}: row-major B == transposed B bitwise: {same}", flush=True)
+    assert same
+    ref = A.double() @ B.double()
+    err = float(((C1.double() - ref).abs().max() / (1 + ref.abs().max())).item())
+    assert err < 1e-5, err
