@@ -143,7 +143,8 @@ int pcd_event_elapsed_ms(float* ms, void* start, void* end);
  * A [m,k] or, with trans_a, the transpose of a physical [k,m] A (same for B).
  * With trans_a = trans_b = 0 and beta = 0 this is MatMulDevice (:62-72).
  * Operands are read where they lie when aligned and whole-tile shaped
- * (16-bit B also in its row-major [k,n] layout, transposed in LDS); others
+ * (16-bit operands in either layout: a row-major B or a transposed A is
+ * transposed in LDS); others
  * are packed into scratch from the library's pool. */
 int pcd_gemm_f32(const float* dA, const float* dB, float* dC, int m, int k, int n,
                  int trans_a, int trans_b, float beta, void* stream);

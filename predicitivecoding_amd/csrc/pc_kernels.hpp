@@ -73,8 +73,10 @@ enum Act { ACT_LINEAR = 0, ACT_TANH = 1, ACT_RELU = 2, ACT_SIGMOID = 3, ACT_GELU
 // layout of Gemm.MatMul's B), read where it lies: each stage's K rows of the
 // tile's columns go into LDS as they are and the MFMA fragments come out of
 // them through gfx950's transposing LDS read (ds_read_b64_tr_b16), so the
-// operand is never packed.  16-bit operands, LDS-operand tiles only.
-enum Epi { EPI_ERROR = 0, EPI_UPDATE = 1, EPI_FFG = 2, EPI_PLAIN = 3, EPI_PLAIN_KN = 4 };
+// operand is never packed.  EPI_PLAIN_MK: the same for an A stored [K x M]
+// (a transposed A); EPI_PLAIN_MKKN: both.  16-bit operands, LDS-operand tiles.
+enum Epi { EPI_ERROR = 0, EPI_UPDATE = 1, EPI_FFG = 2, EPI_PLAIN = 3, EPI_PLAIN_KN = 4, EPI_PLAIN_MK = 5,
+           EPI_PLAIN_MKKN = 6 };
 
 // Global-memory accessors.  The epilogue pointers arrive through the
 // kernel-argument struct as generic pointers; accessing them through the
@@ -340,6 +342,26 @@ template <int RB> __device__ __forceinline__ int swz(int row, int unit) {
 // halves, and the XOR separates k and k + 2.
 template <int BN> __device__ __forceinline__ int kn_swz(int k) {
     return BN >= 128 ? (k & 3) * 4 : ((k >> 1) & 1) * 4;
+}
+// One 32 x 32 x 16 MFMA operand fragment from a stage region that holds K
+// rows of W 16-bit elements (a row-major B, or a transposed A), laid out by
+// kn_swz<W>: lane l takes element x0 + l % 32 of K rows 16c + 8 (l / 32) +
+// 0..7, in two transposing reads of four rows each.  In each group of 16
+// lanes, lane i reads row kbase + i / 4 at elements 4 (i % 4) .. + 3 of the
+// group's 16, and lane j receives element j % 4 of lanes j / 4, 4 + j / 4,
+// 8 + j / 4 and 12 + j / 4, i.e. element j of rows kbase .. kbase + 3.
+template <int W> __device__ __forceinline__ u32x4 tr_fragment(const char* region, int c, int x0) {
+    const int lane = threadIdx.x & 63, half = lane >> 5;
+    const int x = x0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    u32x2 h[2];
+    static_for<0, 2>([&](auto Hc) PCD_INLINE {
+        const int k = 16 * c + 8 * half + 4 * decltype(Hc)::value + ((lane & 15) >> 2);
+        const char* p = region + k * (W * 2) + ((x * 2) ^ (kn_swz<W>(k) * 16));
+        h[decltype(Hc)::value] = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                       (__attribute__((address_space(3))) v4i16*)(__attribute__((address_space(3))) char*)p));
+    });
+    return u32x4{h[0][0], h[0][1], h[1][0], h[1][1]};
 }
 
 // Build-time tile parameters (K bytes per row per stage: *_RB; LDS ring
@@ -944,12 +966,16 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // miss.  The sum over K is taken in that rotated order, so a row's result
     // depends on the row tile it falls in (still the same run to run).
     const int koff = (!C::WD && args.k_stagger > 1 && nk > 0) ? ((tm + tn) % args.k_stagger) % nk : 0;
-    // B row-major [K x N] (EPI_PLAIN_KN): ldb is its row pitch, a stage is KE
-    // of its rows, and the tile's columns start col0 elements into each row.
-    constexpr bool BKN = EPI == EPI_PLAIN_KN;
-    static_assert(!BKN || (OPB == 2 && C::KW == 1 && !C::WD), "row-major B: 16-bit operands, LDS-operand tiles");
+    // B row-major [K x N] (EPI_PLAIN_KN, _MKKN): ldb is its row pitch, a stage
+    // is KE of its rows, and the tile's columns start col0 elements into each
+    // row.  A stored [K x M] (EPI_PLAIN_MK, _MKKN) likewise, with lda and row0.
+    constexpr bool BKN = EPI == EPI_PLAIN_KN || EPI == EPI_PLAIN_MKKN;
+    constexpr bool AKM = EPI == EPI_PLAIN_MK || EPI == EPI_PLAIN_MKKN;
+    static_assert(!(AKM || BKN) || (OPB == 2 && C::KW == 1 && !C::WD),
+                  "operands read through transposing LDS reads: 16-bit operands, LDS-operand tiles");
     const size_t lda_b = (size_t)P.lda * OPB, ldb_b = (size_t)P.ldb * OPB;
-    const char* Ag = (const char*)P.A + (size_t)row0 * lda_b + (size_t)kb * C::RB;
+    const char* Ag = AKM ? (const char*)P.A + (size_t)row0 * OPB + (size_t)kb * KE * lda_b
+                         : (const char*)P.A + (size_t)row0 * lda_b + (size_t)kb * C::RB;
     const char* Bg = BKN ? (const char*)P.B + (size_t)col0 * OPB + (size_t)kb * KE * ldb_b
                          : (const char*)P.B + (size_t)col0 * ldb_b + (size_t)kb * C::RB;
 
@@ -1043,7 +1069,8 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // permuted by kn_swz so that the transposing fragment reads below are
     // conflict-free: the lane that writes region byte ob copies row ob / (BN
     // OPB), unit (ob % (BN OPB)) / 16 ^ kn_swz(row).  A stage then advances
-    // the B source by KE rows.
+    // the B source by KE rows.  A transposed A (AKM) fills the A region (KE
+    // rows of BM elements) the same way.
     const char* src[C::QPW];
 #pragma unroll
     for (int i = 0; i < C::QPW; ++i) {
@@ -1054,11 +1081,16 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
             const int ob = (q * C::ROWS_PER_LOAD - BM) * C::RB + lane * 16;
             const int kr = ob / (BN * OPB);
             src[i] = Bg + (size_t)kr * ldb_b + ((ob % (BN * OPB)) / 16 ^ kn_swz<BN>(kr)) * 16;
+        } else if (AKM && R < BM) {
+            const int ob = q * C::ROWS_PER_LOAD * C::RB + lane * 16;
+            const int kr = ob / (BM * OPB);
+            src[i] = Ag + (size_t)kr * lda_b + ((ob % (BM * OPB)) / 16 ^ kn_swz<BM>(kr)) * 16;
         } else {
             src[i] = R < BM ? Ag + (size_t)R * lda_b + unit * 16 : Bg + (size_t)(R - BM) * ldb_b + unit * 16;
         }
     }
     const size_t bstep = BKN ? (size_t)KE * ldb_b : (size_t)C::RB;   // source bytes per stage of B loads
+    const size_t astep = AKM ? (size_t)KE * lda_b : (size_t)C::RB;   // ... and of A loads
     auto issue_stage = [&](int kt) PCD_INLINE {
         const uint32_t base = lds0 + (kt % C::NS) * C::stage_bytes + wave_u * C::QPW * 1024;
         int kk = kt + koff;
@@ -1066,7 +1098,7 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
 #pragma unroll
         for (int i = 0; i < C::QPW; ++i) {
             const bool bload = (wave_u * C::QPW + i) * 1024 >= BM * C::RB;   // wave-uniform
-            lds_dma16(src[i] + (size_t)kk * (bload ? bstep : (size_t)C::RB), base + i * 1024);
+            lds_dma16(src[i] + (size_t)kk * (bload ? bstep : astep), base + i * 1024);
         }
     };
     // Fragments of K chunk c (32 bytes per row) of the stage in `slot`.
@@ -1074,29 +1106,17 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
         const char* st = smem + slot * C::stage_bytes;
 #pragma unroll
         for (int i = 0; i < C::FM; ++i) {
-            const int R = wm * C::WTM + i * 32 + lr;
-            a[i] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
+            if constexpr (AKM) {
+                a[i] = tr_fragment<BM>(st, c, wm * C::WTM + i * 32);
+            } else {
+                const int R = wm * C::WTM + i * 32 + lr;
+                a[i] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
+            }
         }
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) {
             if constexpr (BKN) {
-                // Lane l takes column n0 + l % 32 and K rows 16c + 8 (l / 32) + 0..7
-                // of the stage, in two transposing reads of four rows each: in each
-                // group of 16 lanes, lane i reads row kbase + i / 4, columns
-                // 4 (i % 4) .. + 3 of the group's 16, and lane j receives element
-                // j % 4 of lanes j / 4, 4 + j / 4, 8 + j / 4 and 12 + j / 4, i.e.
-                // column j of rows kbase .. kbase + 3.
-                const char* bst = st + BM * C::RB;
-                const int n = wn * C::WTN + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-                u32x2 h[2];
-                static_for<0, 2>([&](auto Hc) PCD_INLINE {
-                    const int k = 16 * c + 8 * half + 4 * decltype(Hc)::value + ((lane & 15) >> 2);
-                    const char* p = bst + k * (BN * OPB) + ((n * OPB) ^ (kn_swz<BN>(k) * 16));
-                    h[decltype(Hc)::value] = __builtin_bit_cast(
-                        u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                   (__attribute__((address_space(3))) v4i16*)(__attribute__((address_space(3))) char*)p));
-                });
-                b[j] = u32x4{h[0][0], h[0][1], h[1][0], h[1][1]};
+                b[j] = tr_fragment<BN>(st + BM * C::RB, c, wn * C::WTN + j * 32);
             } else {
                 const int R = BM + wn * C::WTN + j * 32 + lr;
                 b[j] = *(const u32x4*)(st + R * C::RB + swz<C::RB>(R, 2 * c + half) * 16);
@@ -1142,11 +1162,11 @@ __device__ __forceinline__ void phase_unit(KProblem* kprobs, const int nprob, co
     // One LDS fragment read after each of the chunk's first MFMAs, the rest of
     // the MFMAs after them.
     constexpr int NMF = C::FM * C::FN * (F32OP ? 4 : 1);   // MFMAs per chunk
-    constexpr int NRD = C::FM + C::FN * (BKN ? 2 : 1);     // fragment reads per chunk
+    constexpr int NRD = C::FM * (AKM ? 2 : 1) + C::FN * (BKN ? 2 : 1);   // fragment reads per chunk
     auto interleave = [&]() PCD_INLINE {
         // MFMA first: the chunk's first MFMA then waits only on fragments read
         // before it, not on the read just issued (bf16 phases +1%).
-        if constexpr (BKN) {
+        if constexpr (AKM || BKN) {
             constexpr int NP = NMF < NRD ? NMF : NRD;
             static_for<0, NP>([&](auto) PCD_INLINE {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);

@@ -1386,11 +1386,19 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     // B in Gemm.MatMul's own row-major [k x n] layout, with whole tiles of
     // columns and K a whole number of stages, is read where it lies too, on the
     // 16-bit tiles that transpose it in LDS (EPI_PLAIN_KN).
-    const bool kn_b = !trans_b && kn_tile(ob, tile.m, tile.n, false) && n == np && k == kp && aligned(dB);
+    // So is a transposed A (physical [k x m]) on those tiles (EPI_PLAIN_MK).
+    // Except that the transposing reads cost the 128 x 128 tile about a fifth
+    // of its time, more than packing an operand a quarter the other's size or
+    // smaller takes (512 x 8192 x 8192 bf16, A transposed: 0.089 ms in place,
+    // 0.081 packed; the other tiles lose 2-5% and read in place).
+    const bool small_a = tile.m == 128 && (size_t)m * 4 <= (size_t)n;
+    const bool small_b = tile.m == 128 && (size_t)n * 4 <= (size_t)m;
+    const bool kn_b = !trans_b && !small_b && kn_tile(ob, tile.m, tile.n, false) && n == np && k == kp && aligned(dB);
+    const bool mk_a = trans_a && !small_a && kn_tile(ob, tile.m, tile.n, false) && m == mp && k == kp && aligned(dA);
     void *pa = nullptr, *pb = nullptr;
     int st = PCD_SUCCESS;
     auto release = [&]() {
-        if (pa && !direct_a) pool_free(pa, s);
+        if (pa && !direct_a && !mk_a) pool_free(pa, s);
         if (pb && !direct_b && !kn_b) pool_free(pb, s);
     };
     const int src_f32 = dtype == PCD_F32;
@@ -1405,7 +1413,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     // op(A) [m x k]: physical [m x k], or [k x m] when transposed.
     // The kernel's B operand is op(B)^T [n x k]: physical B is [k x n] (read
     // transposed) or, with trans_b, already [n x k].
-    if (direct_a) pa = (void*)dA;
+    if (direct_a || mk_a) pa = (void*)dA;
     else if (!(st = pool_alloc(&pa, (size_t)mp * kp * ob, s))) st = pack(dA, m, k, trans_a, pa, mp, kp);
     if (!st) {
         if (direct_b || kn_b) pb = (void*)dB;
@@ -1416,7 +1424,7 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     sets[0].n = 1;
     Problem& p = sets[0].p[0];
     p.A = pa;
-    p.lda = kp;
+    p.lda = mk_a ? m : kp;   // the row pitch of a transposed A, else of the K-contiguous rows
     p.B = pb;
     p.ldb = kn_b ? n : kp;   // the row pitch of row-major B, else of the K-contiguous copy
     p.M = m;
@@ -1447,7 +1455,8 @@ static int gemm_common(int dtype, const void* dA, const void* dB, float* dC, int
     a.beta = beta;
     a.k_stagger = dtype == PCD_F32 ? 0 : auto_k_stagger(kp / stage_k(dtype, tile));
     a.nt_store = (size_t)m * n * 4 >= kGemmNtBytes;
-    if (!st) st = launch_phase(dtype, tile, kn_b ? EPI_PLAIN_KN : EPI_PLAIN, sets[0], a, s);
+    const int epi = mk_a ? (kn_b ? EPI_PLAIN_MKKN : EPI_PLAIN_MK) : (kn_b ? EPI_PLAIN_KN : EPI_PLAIN);
+    if (!st) st = launch_phase(dtype, tile, epi, sets[0], a, s);
     release();
     if (part) {
         int st2 = pool_free(part, s);
@@ -1477,7 +1486,9 @@ static int gemm_batched_common(int dtype, const void* dA, const void* dB, float*
     // Each B_i [k x n] is read where it lies (EPI_PLAIN_KN) when the tile has
     // that form, its columns fill whole tiles, K is a whole number of stages and
     // every item starts 16-byte aligned.
-    const bool kn_b = kn_tile(ob, tile.m, tile.n, false) && n == np && k == kp && (uintptr_t)dB % 16 == 0;
+    // (and not on the 128 x 128 tile when B_i is a quarter of A_i or smaller: see gemm_common)
+    const bool kn_b = kn_tile(ob, tile.m, tile.n, false) && n == np && k == kp && (uintptr_t)dB % 16 == 0 &&
+                      !(tile.m == 128 && (size_t)n * 4 <= (size_t)m);
     void *pa = nullptr, *pb = nullptr;
     int st = pool_alloc(&pa, a_item * batch, s);
     if (!st && !kn_b) st = pool_alloc(&pb, b_item * batch, s);

@@ -32,11 +32,18 @@ hipError_t launch_phase_tile(int epi, const ProblemSet& set, const PhaseArgs& ar
     case EPI_UPDATE: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_UPDATE, WD>), dim3(grid), block, 0, s, set, args); break;
     case EPI_FFG: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_FFG, WD>), dim3(grid), block, 0, s, set, args); break;
     case EPI_PLAIN_KN:
+    case EPI_PLAIN_MK:
+    case EPI_PLAIN_MKKN:
         if constexpr (kn_tile(OpTraits<OP>::bytes, BM, BN, WD)) {
-            hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN_KN, WD>), dim3(grid), block, 0, s, set, args);
+            if (epi == EPI_PLAIN_KN)
+                hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN_KN, WD>), dim3(grid), block, 0, s, set, args);
+            else if (epi == EPI_PLAIN_MK)
+                hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN_MK, WD>), dim3(grid), block, 0, s, set, args);
+            else
+                hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN_MKKN, WD>), dim3(grid), block, 0, s, set, args);
             break;
         } else {
-            return hipErrorInvalidValue;   // no row-major-B form of this tile
+            return hipErrorInvalidValue;   // no transposed-operand form of this tile
         }
     default: hipLaunchKernelGGL((phase_kernel<OP, BM, BN, EPI_PLAIN, WD>), dim3(grid), block, 0, s, set, args); break;
     }

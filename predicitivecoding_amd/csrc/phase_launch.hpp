@@ -11,8 +11,9 @@
 
 namespace pcd {
 
-// Tiles with a row-major-B plain product (EPI_PLAIN_KN): 16-bit operands on
-// the LDS-operand tiles the GEMM provider uses.
+// Tiles with plain products that read a row-major B or a transposed A in
+// place (EPI_PLAIN_KN, _MK, _MKKN): 16-bit operands on the LDS-operand tiles
+// the GEMM provider uses.
 constexpr bool kn_tile(int op_bytes, int bm, int bn, bool wd) {
     return op_bytes == 2 && !wd && bm == bn && (bm == 64 || bm == 128 || bm == 256);
 }

@@ -802,15 +802,16 @@ def test_gemm_provider_packs_unaligned_operands(dtype, m, k, n, ta, tb):
 
 @pytest.mark.parametrize("dtype,m,k,n", [
     ("bf16", 4096, 1024, 4096),   # 256 x 256 tiles
-    ("f16", 512, 512, 8192),      # 128 x 128
+    ("f16", 2048, 512, 2048),     # 128 x 128
+    ("f16", 512, 512, 8192),      # 128 x 128, the transposed A a sixteenth of B: packed
     ("bf16", 64, 1024, 2048),     # 64 x 64, split-K
     ("f16", 1024, 192, 1024),     # 64 x 64, three K stages
 ])
-def test_gemm_row_major_b_matches_transposed_b_bitwise(dtype, m, k, n):
-    # B in Gemm.MatMul's row-major [k x n] layout, transposed in LDS by the
-    # kernel, against the same B given transposed ([n x k], read as it lies):
-    # the MFMAs see the same operands in the same K order, so the products
-    # agree bit for bit.
+def test_gemm_transposed_operands_match_k_contiguous_bitwise(dtype, m, k, n):
+    # A row-major B ([k x n]) and a transposed A ([k x m]), which the 16-bit
+    # tiles transpose in LDS, against both operands K-contiguous (A [m x k], B
+    # given transposed [n x k], read as they lie): the MFMAs see the same
+    # operands in the same K order, so all four layouts agree bit for bit.
     import torch
     from predicitivecoding_amd import DeviceTensor  # noqa: F401  (loads the library)
     from predicitivecoding_amd._native import call
@@ -819,15 +820,19 @@ def test_gemm_row_major_b_matches_transposed_b_bitwise(dtype, m, k, n):
     g.manual_seed(m + k + n)
     A = torch.randn((m, k), device="cuda", generator=g).to(tdt)
     B = torch.randn((k, n), device="cuda", generator=g).to(tdt)
-    Bt = B.t().contiguous()
-    C1 = torch.empty((m, n), device="cuda", dtype=torch.float32)
-    C2 = torch.empty_like(C1)
-    call(f"pcd_gemm_{dtype}", A.data_ptr(), B.data_ptr(), C1.data_ptr(), m, k, n, 0, 0, 0.0, None)
-    call(f"pcd_gemm_{dtype}", A.data_ptr(), Bt.data_ptr(), C2.data_ptr(), m, k, n, 0, 1, 0.0, None)
+    At, Bt = A.t().contiguous(), B.t().contiguous()
+    out = {}
+    for ta, tb in ((0, 1), (0, 0), (1, 1), (1, 0)):
+        C = torch.empty((m, n), device="cuda", dtype=torch.float32)
+        call(f"pcd_gemm_{dtype}", (At if ta else A).data_ptr(), (Bt if tb else B).data_ptr(), C.data_ptr(),
+             m, k, n, ta, tb, 0.0, None)
+        out[(ta, tb)] = C
     torch.cuda.synchronize()
-    same = torch.equal(C1, C2)
-    print(f"gemm {dtype} {m}x{k}x{n}: row-major B == transposed B bitwise: {same}", flush=True)
-    assert same
+    base = out[(0, 1)]
+    for key, C in out.items():
+        same = torch.equal(C, base)
+        print(f"gemm {dtype} {m}x{k}x{n} trans_a={key[0]} trans_b={key[1]}: bitwise equal {same}", flush=True)
+        assert same, key
     ref = A.double() @ B.double()
-    err = float(((C1.double() - ref).abs().max() / (1 + ref.abs().max())).item())
+    err = float(((base.double() - ref).abs().max() / (1 + ref.abs().max())).item())
     assert err < 1e-5, err
