@@ -114,6 +114,27 @@ def test_every_tile_shape(oracle, dtype, tile):
     assert all(v < tol for v in errs.values()), errs
 
 
+@pytest.mark.parametrize("tile", [(64, 64), (128, 128), (256, 256)])
+def test_cache_policy_options_leave_results_unchanged(oracle, tile):
+    # nt_store / nt_load only choose how the settling epilogues' stores and
+    # state loads treat the caches; the 256 x 256 tile compiles its epilogues
+    # twice (both on, the 16-bit default, and any other setting), so every
+    # setting must give the default's bits.  Ragged shape: partial row and
+    # column tiles on every layer.
+    snap, W, b, P, x = build_case([300, 520, 260, 70], "gelu", 0.1, batch=300, seed=23, init="fanin")
+    base = {"tile": tile[0], "tile_n": tile[1]}
+    ref = run_gpu(snap, x, 5, dtype="bf16", states=True, energy=True, options=base)
+    rtop, _, ren = run_oracle(oracle, snap, W, b, P, x, 5, dtype="bf16", states=True, energy=True)
+    errs = dict(top=max_rel(ref[0], rtop), energy=max_rel(ref[2], ren))
+    _report(f"nt-default/tile{tile}", **errs)
+    assert all(v < 2e-3 for v in errs.values()), errs
+    for st, ld in [(0, 0), (1, 0), (0, 1)]:
+        top, states, en = run_gpu(snap, x, 5, dtype="bf16", states=True, energy=True,
+                                  options=dict(base, nt_store=st, nt_load=ld))
+        assert np.array_equal(top, ref[0]) and np.array_equal(en, ref[2]), (st, ld)
+        assert all(np.array_equal(a, r) for a, r in zip(states, ref[1])), (st, ld)
+
+
 @pytest.mark.parametrize("dtype,stagger", [("f32", 16), ("f32", 3), ("bf16", 0), ("bf16", 16), ("f16", 64)])
 @pytest.mark.parametrize("tile", [(32, 32), (64, 64), (256, 256)])
 def test_k_stagger_parity(oracle, dtype, stagger, tile):
