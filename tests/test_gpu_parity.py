@@ -114,6 +114,29 @@ def test_every_tile_shape(oracle, dtype, tile):
     assert all(v < tol for v in errs.values()), errs
 
 
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("variant", ["plain", "ffg", "actreg_prec"])
+def test_activations_and_options_on_the_256_tile(oracle, act, variant):
+    # The 256 x 256 tile compiles its error and update epilogues once per
+    # activation, with separate branches for lambda = 0 and lambda > 0: each
+    # copy against the same-rounding oracle on a ragged bf16 network (partial
+    # row and column tiles on every layer).
+    kw = dict(ffg=variant == "ffg", act_reg=0.01 if variant == "actreg_prec" else 0.0,
+              precisions=[1.0, 0.7, 1.3, 1.0] if variant == "actreg_prec" else None)
+    snap, W, b, P, x = build_case([300, 260, 130, 40], act, 0.1, batch=260, bias_scale=0.2, seed=41, init="fanin",
+                                  **kw)
+    top, st, en = run_gpu(snap, x, 6, dtype="bf16", states=True, energy=True, options={"tile": 256, "tile_n": 256})
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 6, dtype="bf16", states=True, energy=True)
+    errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren),
+                states=max(max_rel(a, r) for a, r in zip(st, rst)))
+    _report(f"tile256/{act}/{variant}", **errs)
+    # A state within rounding of zero can take the other sign of lambda sign(M)
+    # than the oracle's (16-bit operands round the products that led to it):
+    # that moves it by up to 2 eta lambda in one step, whatever its size.
+    flip = 2 * 0.1 * kw["act_reg"]
+    assert errs["top"] < 2e-3 and errs["energy"] < 2e-3 and errs["states"] < 2e-3 + flip, errs
+
+
 @pytest.mark.parametrize("tile", [(64, 64), (128, 128), (256, 256)])
 def test_cache_policy_options_leave_results_unchanged(oracle, tile):
     # nt_store / nt_load only choose how the settling epilogues' stores and
