@@ -114,22 +114,44 @@ def test_every_tile_shape(oracle, dtype, tile):
     assert all(v < tol for v in errs.values()), errs
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("act", ACTS)
 @pytest.mark.parametrize("variant", ["plain", "ffg", "actreg_prec"])
-def test_activations_and_options_on_the_256_tile(oracle, act, variant):
+def test_activations_and_options_on_the_256_tile(oracle, act, variant, dtype):
     # The 256 x 256 tile compiles its error and update epilogues once per
     # activation, with separate branches for lambda = 0 and lambda > 0: each
-    # copy against the same-rounding oracle on a ragged bf16 network (partial
+    # copy against the same-rounding oracle on a ragged 16-bit network (partial
     # row and column tiles on every layer).
     kw = dict(ffg=variant == "ffg", act_reg=0.01 if variant == "actreg_prec" else 0.0,
               precisions=[1.0, 0.7, 1.3, 1.0] if variant == "actreg_prec" else None)
     snap, W, b, P, x = build_case([300, 260, 130, 40], act, 0.1, batch=260, bias_scale=0.2, seed=41, init="fanin",
                                   **kw)
-    top, st, en = run_gpu(snap, x, 6, dtype="bf16", states=True, energy=True, options={"tile": 256, "tile_n": 256})
-    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 6, dtype="bf16", states=True, energy=True)
+    top, st, en = run_gpu(snap, x, 6, dtype=dtype, states=True, energy=True, options={"tile": 256, "tile_n": 256})
+    rtop, rst, ren = run_oracle(oracle, snap, W, b, P, x, 6, dtype=dtype, states=True, energy=True)
     errs = dict(top=max_rel(top, rtop), energy=max_rel(en, ren),
                 states=max(max_rel(a, r) for a, r in zip(st, rst)))
-    _report(f"tile256/{act}/{variant}", **errs)
+    _report(f"tile256/{dtype}/{act}/{variant}", **errs)
+    if act == "relu":
+        # ReLU's derivative jumps at 0: a pre-activation within rounding of
+        # zero takes one branch or the other with the order of its sum, which
+        # moves that unit's Delta by its whole error.  On this network the
+        # same-rounding oracle is itself 8e-2 (warm start) and 1.1e-1
+        # (regularised) from the fp32 oracle in layer 1's f16 states, and every
+        # tile of the library is 3e-2 and 1e-1 from it.  So the top is held to
+        # the oracle, and the 256 x 256 tile's epilogue copies to the 64 x 64
+        # tile's bit for bit, with both summing K in the same order (no K
+        # stagger, no split-K); the energies sum their row partials in another
+        # order.
+        assert errs["top"] < 2e-3, errs
+        same_order = {"k_stagger": 0, "split_k": 0}
+        big = run_gpu(snap, x, 6, dtype=dtype, states=True, energy=True,
+                      options=dict(same_order, tile=256, tile_n=256))
+        small = run_gpu(snap, x, 6, dtype=dtype, states=True, energy=True,
+                        options=dict(same_order, tile=64, tile_n=64))
+        assert np.array_equal(big[0], small[0])
+        assert all(np.array_equal(p, q) for p, q in zip(big[1], small[1]))
+        assert max_rel(big[2], small[2]) < 1e-5
+        return
     # A state within rounding of zero can take the other sign of lambda sign(M)
     # than the oracle's (16-bit operands round the products that led to it):
     # that moves it by up to 2 eta lambda in one step, whatever its size.
