@@ -59,6 +59,33 @@ int from_hip(hipError_t e, const char* what) {
         if (e_ != hipSuccess) return from_hip(e_, #call); \
     } while (0)
 
+// HIP refuses an operation on the legacy (null) stream, such as a synchronous
+// hipMemcpy, hipMemset or hipDeviceSynchronize, while any stream of the
+// process is capturing a graph, whatever the capture mode, and invalidates
+// that capture too (hipErrorStreamCaptureImplicit, then
+// hipErrorStreamCaptureInvalidated for the capturing thread).  The library's
+// own captures (get_plan) and its legacy-stream calls therefore exclude each
+// other: two callers on two threads, one recording a settling's graph and one
+// copying its inputs, both succeed.  Nothing else is locked while this is held
+// except the pool's mutex inside a capture, and no holder of the pool's mutex
+// waits for this one.
+std::mutex& legacy_stream_mu() {
+    static std::mutex mu;
+    return mu;
+}
+hipError_t sync_memcpy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+    std::lock_guard<std::mutex> g(legacy_stream_mu());
+    return hipMemcpy(dst, src, bytes, kind);
+}
+hipError_t sync_memset(void* dst, int value, size_t bytes) {
+    std::lock_guard<std::mutex> g(legacy_stream_mu());
+    return hipMemset(dst, value, bytes);
+}
+hipError_t device_sync() {
+    std::lock_guard<std::mutex> g(legacy_stream_mu());
+    return hipDeviceSynchronize();
+}
+
 inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 
 // --------------------------------------------------------------- allocator
@@ -399,7 +426,7 @@ int dev_alloc_zero(std::vector<void*>& owned, void** out, size_t bytes) {
     if (bytes == 0) return PCD_SUCCESS;
     HIP_TRY(hipMalloc(out, bytes));
     owned.push_back(*out);
-    HIP_TRY(hipMemset(*out, 0, bytes));
+    HIP_TRY(sync_memset(*out, 0, bytes));
     return PCD_SUCCESS;
 }
 
@@ -421,7 +448,7 @@ int repack_direct(pcd_model* m, int l, hipStream_t s) {
 // that does not keep them (the option that forces the direct-weight tile).
 int alloc_direct(pcd_model* m) {
     HIP_TRY(hipSetDevice(m->device));
-    HIP_TRY(hipDeviceSynchronize());   // the weights may still be written by queued work
+    HIP_TRY(device_sync());   // the weights may still be written by queued work
     std::vector<void*> owned;
     std::vector<void*> wpk(m->L, nullptr), wtpk(m->L, nullptr);
     int st = PCD_SUCCESS;
@@ -434,7 +461,7 @@ int alloc_direct(pcd_model* m) {
         m->Wpk = wpk;
         m->WTpk = wtpk;
         for (int l = 1; l < m->L && !st; ++l) st = repack_direct(m, l, 0);
-        if (!st) st = from_hip(hipDeviceSynchronize(), "direct-weight copies");
+        if (!st) st = from_hip(device_sync(), "direct-weight copies");
         if (!st) return PCD_SUCCESS;
         m->Wpk.clear();
         m->WTpk.clear();
@@ -991,6 +1018,7 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
         if (e != hipSuccess) { *status = from_hip(e, "hipMalloc(energy)"); return nullptr; }
     }
     hipStream_t cs = w->capture;
+    std::unique_lock<std::mutex> no_legacy(legacy_stream_mu());   // no legacy-stream call while recording
     hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) { *status = from_hip(e, "hipStreamBeginCapture"); return nullptr; }
     RelaxSpec rc = r;
@@ -998,6 +1026,7 @@ Plan* get_plan(pcd_model* m, Workspace* w, const RelaxSpec& r, int want_energy, 
     int st = enqueue_relax(m, w, rc, cs, nullptr);
     hipGraph_t g = nullptr;
     e = hipStreamEndCapture(cs, &g);
+    no_legacy.unlock();
     if (st) { if (g) (void)hipGraphDestroy(g); *status = st; return nullptr; }
     if (e != hipSuccess) { *status = from_hip(e, "hipStreamEndCapture"); return nullptr; }
     p->graph = g;
@@ -1187,7 +1216,7 @@ int pcd_get_device(int* device) {
 }
 
 int pcd_device_synchronize(void) {
-    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(device_sync());
     return PCD_SUCCESS;
 }
 
@@ -1239,7 +1268,7 @@ int pcd_host_free(void* ptr) {
 }
 
 int pcd_trim_pools(void) {
-    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(device_sync());
     Pool& P = pool();
     std::lock_guard<std::mutex> g(P.mu);
     for (auto& kv : P.free_blocks)
@@ -1270,7 +1299,7 @@ int pcd_memcpy(void* dst, const void* src, size_t bytes, int kind) {
     if (int st = to_kind(kind, &k)) return st;
     if (bytes == 0) return PCD_SUCCESS;
     if (!dst || !src) return fail(PCD_INVALID_VALUE, "pcd_memcpy: null pointer");
-    HIP_TRY(hipMemcpy(dst, src, bytes, k));
+    HIP_TRY(sync_memcpy(dst, src, bytes, k));
     return PCD_SUCCESS;
 }
 
@@ -1658,9 +1687,9 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
             cleanup();
             return st;
         }
-        hipError_t e = hipMemcpy(tmp, W[l - 1], (size_t)lo * sz * 4, hipMemcpyHostToDevice);
-        if (e == hipSuccess) e = hipMemcpy(bb, b[l - 1], (size_t)lo * 4, hipMemcpyHostToDevice);
-        if (e != hipSuccess) { cleanup(); return from_hip(e, "hipMemcpy(weights)"); }
+        hipError_t e = sync_memcpy(tmp, W[l - 1], (size_t)lo * sz * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = sync_memcpy(bb, b[l - 1], (size_t)lo * 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) { cleanup(); return from_hip(e, "sync_memcpy(weights)"); }
         // W_l as stored ([lo x sz] -> [Rlo x P_l]) and transposed ([sz x lo] -> [Rsz x P_{l-1}]).
         switch (dtype) {
         case PCD_F32:
@@ -1681,7 +1710,7 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
                                m->P[l], m->P[l]);
         e = hipGetLastError();
         if (e == hipSuccess && (st = repack_direct(m.get(), l, 0))) { cleanup(); return st; }
-        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e == hipSuccess) e = device_sync();
         if (e != hipSuccess) { cleanup(); return from_hip(e, "weight packing"); }
         (void)hipFree(tmp);
         owned.pop_back();
@@ -1692,7 +1721,7 @@ int pcd_pc_model_create(const int* sizes, int levels, int activation, float eta,
 
 int pcd_pc_model_destroy(pcd_model* m) {
     if (!m) return PCD_SUCCESS;
-    (void)hipDeviceSynchronize();
+    (void)device_sync();
     for (auto& w : m->ws) free_workspace(*w);
     for (int l = 1; l < m->L; ++l) {
         (void)hipFree(m->W[l]);
@@ -2512,14 +2541,14 @@ int pcd_pc_model_get_weights(pcd_model* m, int layer, float* W_out, float* b_out
     if (layer < 1 || layer >= m->L) return fail(PCD_INVALID_VALUE, "layer %d is not in 1..%d", layer, m->L - 1);
     std::lock_guard<std::mutex> g(m->mu);
     HIP_TRY(hipSetDevice(m->device));
-    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(device_sync());
     const int lo = m->s[layer - 1], sz = m->s[layer];
     if (W_out) {
         const void* src = m->dtype == PCD_F32 ? (const void*)m->W[layer] : (const void*)m->W32[layer];
         HIP_TRY(hipMemcpy2D(W_out, (size_t)sz * 4, src, (size_t)m->P[layer] * 4, (size_t)sz * 4, lo,
                             hipMemcpyDeviceToHost));
     }
-    if (b_out) HIP_TRY(hipMemcpy(b_out, m->bias[layer], (size_t)lo * 4, hipMemcpyDeviceToHost));
+    if (b_out) HIP_TRY(sync_memcpy(b_out, m->bias[layer], (size_t)lo * 4, hipMemcpyDeviceToHost));
     return PCD_SUCCESS;
 }
 
@@ -2573,8 +2602,8 @@ static hipError_t upload_record_weights(pcd_model* m, int layer, const LayerReco
     void* tmp = nullptr;
     hipError_t e = hipMalloc(&tmp, r.weight_bytes);
     if (e != hipSuccess) return e;
-    e = hipMemcpy(tmp, r.weights, r.weight_bytes, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemcpy(m->bias[layer], r.bias, (size_t)lo * 4, hipMemcpyHostToDevice);
+    e = sync_memcpy(tmp, r.weights, r.weight_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = sync_memcpy(m->bias[layer], r.bias, (size_t)lo * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) {
         const float* scales = r.kind == REC_I8 ? (const float*)tmp : nullptr;
         const int8_t* zeros = r.kind == REC_I8 ? (const int8_t*)tmp + (size_t)lo * 4 : nullptr;
@@ -2608,7 +2637,7 @@ static hipError_t upload_record_weights(pcd_model* m, int layer, const LayerReco
                                sz, 0, m->W32[layer], Rlo, m->P[layer]);
         e = hipGetLastError();
         if (e == hipSuccess && repack_direct(m, layer, 0) != PCD_SUCCESS) e = hipErrorLaunchFailure;
-        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e == hipSuccess) e = device_sync();
     }
     (void)hipFree(tmp);
     return e;
@@ -2626,7 +2655,7 @@ int pcd_pc_model_load_record(pcd_model* m, int layer, const void* record, size_t
     if (!(r.precision > 0.f)) return fail(PCD_INVALID_VALUE, "layer record: precision %g is not positive", r.precision);
     std::lock_guard<std::mutex> g(m->mu);
     HIP_TRY(hipSetDevice(m->device));
-    HIP_TRY(hipDeviceSynchronize());   // no settling may read the weights while they change
+    HIP_TRY(device_sync());   // no settling may read the weights while they change
     hipError_t e = hipSuccess;
     if (layer > 0) e = upload_record_weights(m, layer, r);
     if (e != hipSuccess) return from_hip(e, "pcd_pc_model_load_record");

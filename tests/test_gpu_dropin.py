@@ -213,3 +213,51 @@ def test_staged_top_path_under_concurrent_callers(oracle):
             assert all(np.array_equal(g, want[t]) for g in got[t])
     finally:
         m.close()
+
+
+def test_graph_recording_beside_synchronous_copies_on_another_thread(oracle):
+    # HIP refuses a legacy-stream copy (pcd_memcpy) while any stream of the
+    # process records a graph, and then invalidates the recording; the library
+    # keeps its recordings and its synchronous copies apart.  One thread
+    # records a new graph per call (a new step count each time) while another
+    # copies to and from the device the whole time; both get their bits.
+    import threading
+
+    from predicitivecoding_amd import PcDeviceModel, Stream
+    from predicitivecoding_amd.device import DeviceTensor
+    snap, _, _, _ = _trained_snapshot(oracle, seed=43)
+    m = PcDeviceModel(snap, "f32")
+    x = make_inputs(40, 6, seed=300, dist="uniform11")
+    steps = list(range(3, 15))
+    want = [m.relax(x, t)[0] for t in steps]
+    errors, stop = [], threading.Event()
+
+    def copier():
+        buf = np.arange(4096, dtype=np.float32)
+        try:
+            while not stop.is_set():
+                t = DeviceTensor.from_host(buf)
+                try:
+                    if not np.array_equal(t.to_host(), buf):
+                        raise AssertionError("copy came back changed")
+                finally:
+                    t.free()
+        except Exception as e:   # reported below
+            errors.append(e)
+
+    th = threading.Thread(target=copier)
+    th.start()
+    s = Stream()
+    got = []
+    try:
+        for t in steps:
+            got.append(m.relax(x, t, stream=s)[0])
+    except Exception as e:   # reported below
+        errors.append(e)
+    finally:
+        stop.set()
+        th.join(timeout=60)
+        s.close()
+        m.close()
+    assert not errors, errors
+    assert all(np.array_equal(g, w) for g, w in zip(got, want))
