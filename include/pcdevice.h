@@ -17,7 +17,11 @@
  *     and is complete only after a synchronisation.
  * Thread safety: distinct streams may be used from distinct threads; a model
  * handle is immutable after creation; the per-call scratch belongs to the
- * (model, stream) pair.
+ * (model, stream) pair.  A call that records its settling into a HIP graph
+ * (the first call of a shape on a stream) and the library's synchronous copies
+ * (pcd_memcpy, weight uploads) exclude each other, because HIP fails a
+ * legacy-stream operation made while any stream of the process is recording;
+ * a caller's own legacy-stream calls made meanwhile are not covered.
  */
 #ifndef PCDEVICE_H
 #define PCDEVICE_H
